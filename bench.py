@@ -1,0 +1,211 @@
+"""Benchmark: page-wise decode attention on one MI355X.
+
+Headline workload: Llama-3-8B-shape decode, batch 64 x 8192-token contexts,
+32 Q / 8 KV heads, head_dim 128, F16, 16-token pages randomly permuted in a
+32768-page pool.  One step = one batched attention call over the whole batch
+(one layer, one decode step), inputs resident in HBM.  Prints ONE JSON line.
+
+  python bench.py [--steps K] [--warmup W] [--gpus 1] [--skip-cpu] [--only-headline]
+"""
+import argparse
+import ctypes
+import json
+import os
+import platform
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "mini-vllm-rs_amd"))
+
+HBM_PEAK_GBS = 8000.0      # MI355X HBM3E, 8 TB/s
+MFMA_F16_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 MFMA
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "hbm_traffic.json")
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+class Runner:
+    """Prebuilt C argument block for repeated calls (no per-call Python work beyond one ctypes call)."""
+
+    def __init__(self, w, tensors, torch, M):
+        self.w = w
+        self.t = tensors
+        self.out = torch.empty_like(tensors["q"])
+        self.args = M.make_args(tensors["q"], tensors["key_pool"], tensors["value_pool"], tensors["block_tables"],
+                                tensors["seq_lens"], tensors["cu_q_lens"], self.out, max_q_len=w.max_q_len,
+                                max_seq_len=w.max_seq_len)
+        need = M.workspace_size(self.args)
+        self.ws = torch.empty(max(need, 256), dtype=torch.uint8, device="cuda")
+        self.args.workspace = self.ws.data_ptr()
+        self.args.workspace_bytes = need
+        self.lib = M.load_library()
+        self.M = M
+
+    def step(self):
+        rc = self.lib.mvr_paged_attention(ctypes.byref(self.args))
+        if rc != 0:
+            raise self.M.MvrError(rc, self.lib.mvr_last_error().decode())
+
+
+def time_steps(runner, torch, steps, warmup):
+    for _ in range(warmup):
+        runner.step()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        starts[i].record(stream)
+        runner.step()
+        ends[i].record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    per = sorted(s.elapsed_time(e) * 1e3 for s, e in zip(starts, ends))  # microseconds, kernel-side
+    return wall, per
+
+
+def cpu_baseline(W):
+    """The oracle (C restatement of forward_paged_attention, reference dataflow with f16-rounded
+    intermediates) on a bounded sample of the headline workload: 8 of the 64 sequences, all 8 kv heads,
+    all 8192 tokens, repeated for about 10 s on the host cores available to this process (at most 16).
+    Reported in the headline unit (effective KV-read GB/s)."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import numpy as np
+
+    import oracle
+
+    oracle.build()
+    full = W.llama3_8b_decode_b64_8k_f16()
+    sample = W.llama3_8b_decode_b64_8k_f16(batch=8)
+    q, k, v = W.host_values(sample)
+    threads = min(len(os.sched_getaffinity(0)), 16)
+    reps = 0
+    t0 = time.perf_counter()
+    while True:
+        oracle.paged_attention(q, k, v, sample.block_tables, sample.seq_lens, sample.cu_q_lens, sample.num_q_heads,
+                               sample.num_kv_heads, sample.head_dim, sample.page_size, dtype=oracle.F16,
+                               num_threads=threads)
+        reps += 1
+        el = time.perf_counter() - t0
+        if el > 10.0:
+            break
+    per_call = el / reps
+    gbs = sample.algorithmic_bytes() / per_call / 1e9
+    return dict(value=round(gbs, 3), unit="GB/s", cores=threads, kind="port",
+                sample=f"{sample.num_seqs} of {full.num_seqs} sequences x 8 kv heads x 8192 tokens (F16 reference dataflow, "
+                       f"{reps} calls, {per_call * 1e3:.1f} ms/call; full batch extrapolates to "
+                       f"{per_call * full.num_seqs / sample.num_seqs * 1e3:.0f} ms/step)",
+                host=platform.processor() or platform.machine())
+
+
+def measure(W, M, torch, cfg, steps, warmup):
+    w = W.CONFIGS[cfg]()
+    t = W.device_tensors(w, None)
+    r = Runner(w, t, torch, M)
+    wall, per = time_steps(r, torch, steps, warmup)
+    med = per[len(per) // 2]
+    mean = sum(per) / len(per)
+    res = dict(workload=w.name, us_per_step_median=round(med, 2), us_per_step_mean=round(mean, 2),
+               wall_us_per_step=round(wall / steps * 1e6, 2), bytes=w.algorithmic_bytes(),
+               eff_gbs=round(w.algorithmic_bytes() / (med * 1e-6) / 1e9, 1))
+    if w.shared_pages:
+        res["unique_bytes"] = w.algorithmic_bytes(unique=True)
+        res["unique_gbs"] = round(w.algorithmic_bytes(unique=True) / (med * 1e-6) / 1e9, 1)
+        res["hbm_frac"] = round(res["unique_gbs"] / HBM_PEAK_GBS, 4)
+    else:
+        res["hbm_frac"] = round(res["eff_gbs"] / HBM_PEAK_GBS, 4)
+    if cfg == 4:
+        res["tflops"] = round(w.flops() / (med * 1e-6) / 1e12, 2)
+        res["mfma_frac"] = round(res["tflops"] / MFMA_F16_PEAK_TFLOPS, 4)
+    del t, r
+    torch.cuda.empty_cache()
+    return res
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--skip-cpu", action="store_true")
+    ap.add_argument("--only-headline", action="store_true")
+    a = ap.parse_args()
+    if a.gpus != 1:
+        print(f"bench.py measures one GPU only; --gpus {a.gpus} is not supported (this path is single-GPU; "
+              "see the sharding notes in DESIGN.md)", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    import mvr_attn as M
+    import workloads as W
+
+    if not torch.cuda.is_available():
+        print("no GPU visible", file=sys.stderr)
+        sys.exit(1)
+    M.load_library()
+    headline_cfg = 3
+    w = W.CONFIGS[headline_cfg]()
+    log(f"[bench] headline: {w.name}")
+    t = W.device_tensors(w, None)
+    r = Runner(w, t, torch, M)
+    wall, per = time_steps(r, torch, a.steps, a.warmup)
+    med = per[len(per) // 2]
+    mean = sum(per) / len(per)
+    alg = w.algorithmic_bytes()
+    value = alg / (mean * 1e-6) / 1e9
+    log(f"[bench] headline median {med:.1f} us, mean {mean:.1f} us, {value:.0f} GB/s")
+    del t, r
+    torch.cuda.empty_cache()
+
+    traffic = None
+    if os.path.exists(TRAFFIC_FILE):
+        with open(TRAFFIC_FILE) as f:
+            traffic = json.load(f).get("bytes_per_launch")
+
+    result = {
+        "metric": "decode attention us/step + effective KV-read GB/s (% HBM peak), 1 MI355X",
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": a.steps,
+        "warmup": a.warmup,
+        "ms_per_step": round(mean / 1e3, 4),
+        "us_per_step": round(mean, 2),
+        "us_per_step_median": round(med, 2),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16",
+        "data": "synthetic (seeded N(0,1)*0.3 values, seeded page permutation)",
+        "config": dict(w.describe(), workload="llama3-8b-shape paged decode attention, batch 64 x 8192 ctx, "
+                                             "32q/8kv heads, head_dim 128, 16-token pages, f16"),
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(value, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(value / HBM_PEAK_GBS, 4),
+            "traffic": traffic,
+            "timed": "whole attention call (split-context kernel + partition merge), HIP events on the launch stream",
+        },
+    }
+    if not a.only_headline:
+        per_cfg = {}
+        for cfg in (1, 2, 4, 5):
+            log(f"[bench] config {cfg}")
+            per_cfg[str(cfg)] = measure(W, M, torch, cfg, max(20, a.steps // 2), a.warmup)
+        result["configs"] = per_cfg
+    if not a.skip_cpu:
+        log("[bench] cpu baseline")
+        result["cpu_baseline"] = cpu_baseline(W)
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

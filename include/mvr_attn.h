@@ -1,0 +1,153 @@
+/*
+ * mvr_attn — MI355X (gfx950) page-wise attention over a paged KV cache.
+ *
+ * C ABI for mini-vllm-rs's attention hot path.  It replaces
+ *   - the CPU-only page-wise attention, forward_paged_attention
+ *     (src/models/backends/common.rs:739-817, reached through
+ *     forward_cpu_paged_attention, common.rs:426-464), and
+ *   - the GPU gather-to-contiguous fallback, reconstruct_contiguous_tensor
+ *     (src/model_runner/server/kv_cache/paged_cache.rs:363-391) followed by
+ *     forward_contiguous_attention (common.rs:703-737).
+ *
+ * Data contract (src/models/mod.rs:56-100, kv_cache/utils.rs:55-74):
+ *   key_pool / value_pool: [num_pages, 1, num_kv_heads, page_size, head_dim],
+ *     contiguous, in the activation dtype (F32 or F16).
+ *   block_tables: int32 [num_seqs, max_pages_per_seq]; row s holds the
+ *     request's page_ids in logical order (PagedCacheLayout::page_ids).
+ *   seq_lens: int32 [num_seqs] = cached_token_count, which already includes
+ *     the request's current query tokens (common.rs:447-454).
+ *   cu_q_lens: int32 [num_seqs + 1], prefix sums of q_len
+ *     (ForwardContext::q_start_index, common.rs:603-626).
+ *   q / out: element (q head h, packed token n, dim d) at
+ *     h*stride_head + n*stride_token + d.  The reference's packed layout
+ *     [1, Hq, packed_q_len, D] has stride_head = packed_q_len*D,
+ *     stride_token = D (common.rs:268-275, 326-332).
+ *   Q head h reads KV head h / (num_q_heads / num_kv_heads)
+ *     (common.rs:819-859).
+ *   Query i of a request (0-based within the request) sees keys
+ *     0 ..= seq_len - q_len + i (common.rs:948-965).
+ *
+ * Every call is stream-ordered and asynchronous, allocates nothing and keeps
+ * no global mutable state besides a thread-local error string, so several
+ * threads may drive several devices concurrently.  Functions return MVR_OK
+ * (0) or a negative MVR_E_* code; mvr_last_error() describes the last
+ * failure on the calling thread.
+ */
+#ifndef MVR_ATTN_H
+#define MVR_ATTN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MVR_ATTN_ABI_VERSION 1
+
+/* ActivationDType (src/model_runner/mod.rs:331-351): F32 or F16 only. */
+typedef enum { MVR_DTYPE_F32 = 0, MVR_DTYPE_F16 = 1 } mvr_dtype;
+
+typedef enum {
+  MVR_OK = 0,
+  MVR_E_INVALID_ARGUMENT = -1,
+  MVR_E_UNSUPPORTED = -2,
+  /* common.rs:447-454: "paged KV cache reports sequence length X, expected Y" */
+  MVR_E_LENGTH_MISMATCH = -3,
+  /* common.rs:776-781: "paged KV cache contains fewer pages than its sequence
+     length, leaving N tokens uncovered" */
+  MVR_E_PAGES_UNCOVERED = -4,
+  /* a page id outside [0, num_pages) (Tensor::narrow fails in the reference) */
+  MVR_E_PAGE_ID = -5,
+  MVR_E_WORKSPACE = -6,
+  MVR_E_HIP = -7
+} mvr_status;
+
+typedef struct mvr_paged_attention_args {
+  int32_t dtype;             /* mvr_dtype */
+  int32_t num_seqs;          /* requests packed in this call, >= 1 */
+  int32_t num_q_heads;
+  int32_t num_kv_heads;      /* divides num_q_heads */
+  int32_t head_dim;          /* 64 or 128 */
+  int32_t page_size;         /* per_page_token_count; a multiple of 16 */
+  int64_t num_pages;         /* page_count of each pool */
+  int32_t max_pages_per_seq; /* row stride of block_tables */
+  int32_t max_q_len;         /* >= every q_len (host-side bound, sizes the grid) */
+  int32_t max_seq_len;       /* >= every seq_len (host-side bound, sizes the grid) */
+  float scale;               /* softmax scale; 0 selects 1/sqrt(head_dim) as the reference does */
+  const void* q;
+  int64_t q_stride_head;     /* elements */
+  int64_t q_stride_token;    /* elements */
+  const void* key_pool;
+  const void* value_pool;
+  const int32_t* block_tables; /* device */
+  const int32_t* seq_lens;     /* device; NULL allowed when num_seqs == 1: seq_len = max_seq_len */
+  const int32_t* cu_q_lens;    /* device; NULL allowed when num_seqs == 1: q_len = max_q_len */
+  void* out;
+  int64_t out_stride_head;   /* elements */
+  int64_t out_stride_token;  /* elements */
+  void* workspace;           /* device scratch for split-context partials */
+  size_t workspace_bytes;
+  void* stream;              /* hipStream_t; NULL = the null stream */
+} mvr_paged_attention_args;
+
+/* Bytes of workspace mvr_paged_attention needs for these arguments (depends
+   only on the scalar fields).  May be 0. */
+size_t mvr_paged_attention_workspace_size(const mvr_paged_attention_args* args);
+
+/* Batched page-wise attention (decode, speculative verification and chunked
+   prefill in one entry point).  Replaces forward_paged_attention
+   (common.rs:739-817) for every request of a layer in one launch sequence,
+   removing the per-request loop of forward_attention (common.rs:285-327).
+   Checks the scalar arguments on the host; device tables are trusted (see
+   mvr_paged_attention_validate). */
+int mvr_paged_attention(const mvr_paged_attention_args* args);
+
+/* Host-side checks of the tables the device will read, mirroring the
+   reference's errors: seq_len == cached_kv_len + q_len >= q_len >= 1
+   (common.rs:447-454), pages covering every length (common.rs:776-781),
+   page ids inside the pool.  Host copies of the tables; any may be NULL to
+   skip its checks.  Launches nothing. */
+int mvr_paged_attention_validate(const mvr_paged_attention_args* args, const int32_t* block_tables_host,
+                                 const int32_t* seq_lens_host, const int32_t* cu_q_lens_host);
+
+/* AttentionDimensions (common.rs:189-206). */
+typedef struct mvr_attention_dimensions {
+  int32_t num_q_heads;
+  int32_t num_kv_heads;
+  int32_t head_dim;
+  int32_t cached_kv_len;
+  int32_t q_len;
+} mvr_attention_dimensions;
+
+/* PagedCacheLayout (src/models/mod.rs:94-100) with the page ids already on
+   the device as int32. */
+typedef struct mvr_paged_cache_layout {
+  const void* key_pool;
+  const void* value_pool;
+  int64_t page_count;
+  const int32_t* page_ids; /* device */
+  int32_t num_page_ids;
+  int32_t per_page_token_count;
+  int32_t cached_token_count;
+} mvr_paged_cache_layout;
+
+/* Request-level entry with the reference's signature and checks
+   (forward_cpu_paged_attention + forward_paged_attention,
+   common.rs:426-464 and :739-817): request_q and request_y are
+   [1, num_q_heads, q_len, head_dim] contiguous. */
+int mvr_forward_paged_attention(int32_t dtype, const mvr_attention_dimensions* dims,
+                                const mvr_paged_cache_layout* layout, const void* request_q, void* request_y,
+                                void* workspace, size_t workspace_bytes, void* stream);
+size_t mvr_forward_paged_attention_workspace_size(int32_t dtype, const mvr_attention_dimensions* dims,
+                                                  const mvr_paged_cache_layout* layout);
+
+/* Thread-local description of the last error on this thread ("" if none). */
+const char* mvr_last_error(void);
+
+int mvr_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* MVR_ATTN_H */

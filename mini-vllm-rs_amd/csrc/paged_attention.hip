@@ -1,0 +1,470 @@
+// Page-wise attention kernels for gfx950 (MI355X, CDNA4).
+//
+// Replaces forward_paged_attention (src/models/backends/common.rs:739-817)
+// and the GPU gather fallback (paged_cache.rs:363-391 + common.rs:703-737).
+//
+// Work decomposition: one wavefront per unit = (sequence b, kv head h, row
+// tile rt, context partition).  A row tile holds 16*ROW_BLOCKS grouped query
+// rows rho = r*q_len + i of kv head h (query head h*group_size + r, query
+// position i), so every K/V element a wavefront reads from HBM feeds all the
+// query heads that share it (GQA).  The context is walked in 16-token chunks
+// read directly from the pools through the block table:
+//   * K chunk -> registers in the MFMA A-operand layout (lane l holds token
+//     l%16, 8 dims per 16-byte load), S^T = K Q^T with
+//     v_mfma_f32_16x16x32_f16 (f16) or v_mfma_f32_16x16x4_f32 (f32);
+//   * S^T lands with lane l owning query row l%16 and tokens 4*(l/16)+i, so
+//     the online softmax (exp2 domain, fp32 state) needs only two cross-lane
+//     max steps per chunk;
+//   * V chunk -> 16-byte loads -> a swizzled LDS tile -> ds_read_b64_tr_b16
+//     returns V^T in the A-operand layout, O^T += V^T P^T with
+//     v_mfma_f32_16x16x16_f16 (f32: ds_read_b32 + v_mfma_f32_16x16x4_f32).
+// Loads for chunk k+2 are issued before chunk k is consumed (two chunks in
+// flight per wavefront).  Partitions of one (b, h, rt) are merged by
+// merge_partitions_kernel with the usual max / sum-of-exponentials rescale.
+#include "paged_attention_kernels.hpp"
+
+#include <math.h>
+
+namespace mvr {
+namespace {
+
+typedef _Float16 half_t;
+typedef half_t half8 __attribute__((ext_vector_type(8)));
+typedef half_t half4 __attribute__((ext_vector_type(4)));
+typedef short short4v __attribute__((ext_vector_type(4)));
+typedef float float4v __attribute__((ext_vector_type(4)));
+
+typedef __attribute__((address_space(3))) short4v lds_short4;
+
+__device__ __forceinline__ int lane_id() { return __lane_id(); }
+
+__device__ __forceinline__ float wave_max_across_groups(float v) {
+  // Lanes l, l^16, l^32, l^48 hold the same query row.
+  v = fmaxf(v, __shfl_xor(v, 16));
+  v = fmaxf(v, __shfl_xor(v, 32));
+  return v;
+}
+
+__device__ __forceinline__ float wave_sum_across_groups(float v) {
+  v += __shfl_xor(v, 16);
+  v += __shfl_xor(v, 32);
+  return v;
+}
+
+// Per-sequence metadata (seq_lens / cu_q_lens may be absent for one request).
+struct SeqInfo {
+  int seq_len, q_start, q_len;
+};
+
+__device__ __forceinline__ SeqInfo load_seq(const PagedAttentionParams& p, int b) {
+  SeqInfo s;
+  s.seq_len = p.seq_lens ? p.seq_lens[b] : p.single_seq_len;
+  if (p.cu_q_lens) {
+    s.q_start = p.cu_q_lens[b];
+    s.q_len = p.cu_q_lens[b + 1] - s.q_start;
+  } else {
+    s.q_start = 0;
+    s.q_len = p.single_q_len;
+  }
+  return s;
+}
+
+// Number of 16-token chunks row tile rt of a sequence must visit: keys up to
+// the largest causal limit among its rows (key j visible to query i iff
+// j <= seq_len - q_len + i, common.rs:948-965).
+__device__ __forceinline__ int tile_chunks(const SeqInfo& s, int group_size, int rt, int tile_rows) {
+  const int rows = group_size * s.q_len;
+  const int rho0 = rt * tile_rows;
+  if (rho0 >= rows || s.q_len <= 0) return 0;
+  const int rho1 = min(rho0 + tile_rows, rows) - 1;
+  const int max_i = (rho1 / s.q_len != rho0 / s.q_len) ? s.q_len - 1 : rho1 % s.q_len;
+  const int last_key = s.seq_len - s.q_len + max_i;
+  return last_key / kChunkTokens + 1;
+}
+
+// ---------------------------------------------------------------------------
+// dtype traits: how a 16-token chunk is loaded, multiplied and staged.
+// ---------------------------------------------------------------------------
+
+template <int D>
+struct F16Traits {
+  typedef half_t elem;
+  static constexpr int kLoads = D / 32;   // 16-byte K loads (and V loads) per lane per chunk
+  static constexpr int kQRegs = D / 32;   // half8 Q operand registers per row block
+  typedef half8 kreg_t;
+  typedef half8 vreg_t;
+  typedef half8 qreg_t;
+
+  // 32-byte pieces of an LDS row: D/16; XOR swizzle spreads 16 rows over banks.
+  __device__ static __forceinline__ int swz(int t) { return D == 128 ? (t & 7) : ((t >> 1) & 3); }
+
+  __device__ static __forceinline__ void load_q(const half_t* row, bool valid, int g, qreg_t (&q)[kQRegs]) {
+#pragma unroll
+    for (int s = 0; s < kQRegs; s++) {
+      q[s] = valid ? *reinterpret_cast<const half8*>(row + 8 * g + 32 * s) : half8{};
+    }
+  }
+
+  __device__ static __forceinline__ void load_k(const half_t* slab, int l, kreg_t (&k)[kLoads]) {
+    const half_t* row = slab + (l & 15) * D + 8 * (l >> 4);
+#pragma unroll
+    for (int s = 0; s < kLoads; s++) k[s] = *reinterpret_cast<const half8*>(row + 32 * s);
+  }
+
+  __device__ static __forceinline__ void load_v(const half_t* slab, int l, vreg_t (&v)[kLoads]) {
+#pragma unroll
+    for (int u = 0; u < kLoads; u++) {
+      const int ci = l + 64 * u; // 16-byte chunk of the 16 x D slab
+      v[u] = *reinterpret_cast<const half8*>(slab + 8 * ci);
+    }
+  }
+
+  __device__ static __forceinline__ void stage_v(half_t* lds, int l, int tok_valid, const vreg_t (&v)[kLoads]) {
+#pragma unroll
+    for (int u = 0; u < kLoads; u++) {
+      const int ci = l + 64 * u;
+      const int t = ci / (D / 8), c = ci % (D / 8);
+      const int piece = (c >> 1) ^ swz(t);
+      // Slots past the sequence end may hold anything (unwritten pages);
+      // zero them so 0-weight * garbage cannot produce NaN.
+      half8 val = t < tok_valid ? v[u] : half8{};
+      *reinterpret_cast<half8*>(lds + t * D + piece * 16 + (c & 1) * 8) = val;
+    }
+  }
+
+  __device__ static __forceinline__ float4v qk(const kreg_t (&k)[kLoads], const qreg_t (&q)[kQRegs]) {
+    float4v acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < kLoads; s++) acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(k[s], q[s], acc, 0, 0, 0);
+    return acc;
+  }
+
+  template <int NB>
+  __device__ static __forceinline__ void pv(half_t* lds, int l, const float (&p)[NB][4], float4v (&o)[NB][D / 16]) {
+    half4 pb[NB];
+#pragma unroll
+    for (int nb = 0; nb < NB; nb++) pb[nb] = half4{(half_t)p[nb][0], (half_t)p[nb][1], (half_t)p[nb][2], (half_t)p[nb][3]};
+    const int g = l >> 4, qd = l & 15;
+    const int row = 4 * g + (qd >> 2);
+    const int sw = swz(row);
+#pragma unroll
+    for (int n = 0; n < D / 16; n++) {
+      half_t* addr = lds + row * D + ((n ^ sw) * 16) + 4 * (qd & 3);
+      short4v raw = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4*)(addr));
+      half4 vt = __builtin_bit_cast(half4, raw);
+#pragma unroll
+      for (int nb = 0; nb < NB; nb++) o[nb][n] = __builtin_amdgcn_mfma_f32_16x16x16f16(vt, pb[nb], o[nb][n], 0, 0, 0);
+    }
+  }
+
+  __device__ static __forceinline__ void store_out(half_t* dst, float4v v) {
+    half4 h = {(half_t)v[0], (half_t)v[1], (half_t)v[2], (half_t)v[3]};
+    *reinterpret_cast<half4*>(dst) = h;
+  }
+};
+
+template <int D>
+struct F32Traits {
+  typedef float elem;
+  static constexpr int kLoads = D / 16; // 16-byte loads per lane per chunk
+  static constexpr int kQRegs = D / 16;
+  typedef float4v kreg_t;
+  typedef float4v vreg_t;
+  typedef float4v qreg_t;
+
+  // 64-byte pieces (16 floats) of an LDS row; rows 4g+j of the four lane
+  // groups land in four different pieces.
+  __device__ static __forceinline__ int swz(int t) { return (t >> 2) & 3; }
+
+  __device__ static __forceinline__ void load_q(const float* row, bool valid, int g, qreg_t (&q)[kQRegs]) {
+#pragma unroll
+    for (int u = 0; u < kQRegs; u++) {
+      q[u] = valid ? *reinterpret_cast<const float4v*>(row + 16 * u + 4 * g) : float4v{0.f, 0.f, 0.f, 0.f};
+    }
+  }
+
+  __device__ static __forceinline__ void load_k(const float* slab, int l, kreg_t (&k)[kLoads]) {
+    const float* row = slab + (l & 15) * D + 4 * (l >> 4);
+#pragma unroll
+    for (int u = 0; u < kLoads; u++) k[u] = *reinterpret_cast<const float4v*>(row + 16 * u);
+  }
+
+  __device__ static __forceinline__ void load_v(const float* slab, int l, vreg_t (&v)[kLoads]) {
+#pragma unroll
+    for (int u = 0; u < kLoads; u++) v[u] = *reinterpret_cast<const float4v*>(slab + 4 * (l + 64 * u));
+  }
+
+  __device__ static __forceinline__ void stage_v(float* lds, int l, int tok_valid, const vreg_t (&v)[kLoads]) {
+#pragma unroll
+    for (int u = 0; u < kLoads; u++) {
+      const int ci = l + 64 * u;
+      const int t = ci / (D / 4), c = ci % (D / 4);
+      const int piece = (c >> 2) ^ swz(t);
+      float4v val = t < tok_valid ? v[u] : float4v{0.f, 0.f, 0.f, 0.f};
+      *reinterpret_cast<float4v*>(lds + t * D + piece * 16 + (c & 3) * 4) = val;
+    }
+  }
+
+  __device__ static __forceinline__ float4v qk(const kreg_t (&k)[kLoads], const qreg_t (&q)[kQRegs]) {
+    float4v acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int u = 0; u < kLoads; u++) {
+#pragma unroll
+      for (int e = 0; e < 4; e++) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(k[u][e], q[u][e], acc, 0, 0, 0);
+    }
+    return acc;
+  }
+
+  template <int NB>
+  __device__ static __forceinline__ void pv(float* lds, int l, const float (&p)[NB][4], float4v (&o)[NB][D / 16]) {
+    const int g = l >> 4, qd = l & 15;
+#pragma unroll
+    for (int n = 0; n < D / 16; n++) {
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        const int row = 4 * g + j;
+        const float vt = lds[row * D + ((n ^ swz(row)) * 16) + qd];
+#pragma unroll
+        for (int nb = 0; nb < NB; nb++) o[nb][n] = __builtin_amdgcn_mfma_f32_16x16x4f32(vt, p[nb][j], o[nb][n], 0, 0, 0);
+      }
+    }
+  }
+
+  __device__ static __forceinline__ void store_out(float* dst, float4v v) { *reinterpret_cast<float4v*>(dst) = v; }
+};
+
+// ---------------------------------------------------------------------------
+// Split-context paged attention: one wavefront per unit.
+// ---------------------------------------------------------------------------
+template <typename Tr, int D, int NB>
+__global__ __launch_bounds__(kWaveSize* kWavesPerBlock) void paged_attention_kernel(PagedAttentionParams p) {
+  typedef typename Tr::elem T;
+  constexpr int kTileRows = 16 * NB;
+  __shared__ __attribute__((aligned(16))) T lds_all[kWavesPerBlock][kChunkTokens * D];
+
+  const int l = lane_id();
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWaveSize);
+  const int64_t unit = (int64_t)blockIdx.x * kWavesPerBlock + wave;
+  if (unit >= p.num_units) return;
+  T* lds = lds_all[wave];
+
+  int64_t rest = unit;
+  const int part = (int)(rest % p.max_parts);
+  rest /= p.max_parts;
+  const int rt = (int)(rest % p.row_tiles);
+  rest /= p.row_tiles;
+  const int h = (int)(rest % p.num_kv_heads);
+  const int b = (int)(rest / p.num_kv_heads);
+
+  const SeqInfo s = load_seq(p, b);
+  const int rows = p.group_size * s.q_len;
+  const int n_chunks = tile_chunks(s, p.group_size, rt, kTileRows);
+  const int k0 = part * p.chunks_per_part;
+  if (n_chunks == 0 || k0 >= n_chunks) return;
+  const int k1 = min(k0 + p.chunks_per_part, n_chunks);
+  const int n_parts = (n_chunks + p.chunks_per_part - 1) / p.chunks_per_part;
+  const int g = l >> 4;
+
+  // Query rows of this lane (one per row block) and their causal limits.
+  typename Tr::qreg_t q[NB][Tr::kQRegs];
+  int limit[NB];
+  bool row_valid[NB];
+  int q_head[NB], q_tok[NB];
+#pragma unroll
+  for (int nb = 0; nb < NB; nb++) {
+    const int rho = rt * kTileRows + nb * 16 + (l & 15);
+    row_valid[nb] = rho < rows;
+    const int r = row_valid[nb] ? rho / s.q_len : 0;
+    const int i = row_valid[nb] ? rho % s.q_len : 0;
+    q_head[nb] = h * p.group_size + r;
+    q_tok[nb] = s.q_start + i;
+    limit[nb] = row_valid[nb] ? s.seq_len - s.q_len + i : s.seq_len - 1;
+    const T* qrow = static_cast<const T*>(p.q) + (int64_t)q_head[nb] * p.q_stride_head + (int64_t)q_tok[nb] * p.q_stride_token;
+    Tr::load_q(qrow, row_valid[nb], g, q[nb]);
+  }
+
+  float m[NB], lsum[NB];
+  float4v o[NB][D / 16];
+#pragma unroll
+  for (int nb = 0; nb < NB; nb++) {
+    m[nb] = -INFINITY;
+    lsum[nb] = 0.f;
+#pragma unroll
+    for (int n = 0; n < D / 16; n++) o[nb][n] = float4v{0.f, 0.f, 0.f, 0.f};
+  }
+
+  const T* kpool = static_cast<const T*>(p.key_pool);
+  const T* vpool = static_cast<const T*>(p.value_pool);
+  const int32_t* bt = p.block_tables + (int64_t)b * p.block_table_stride;
+  const int chunks_per_page = p.page_size / kChunkTokens;
+
+  auto slab_offset = [&](int k) -> int64_t {
+    const int page = __builtin_amdgcn_readfirstlane(bt[k / chunks_per_page]);
+    const int slot0 = (k % chunks_per_page) * kChunkTokens;
+    return (((int64_t)page * p.num_kv_heads + h) * p.page_size + slot0) * D;
+  };
+
+  auto process = [&](int k, const typename Tr::kreg_t (&kr)[Tr::kLoads], const typename Tr::vreg_t (&vr)[Tr::kLoads]) {
+    const int tok0 = k * kChunkTokens;
+    asm volatile("" ::: "memory");
+    Tr::stage_v(lds, l, s.seq_len - tok0, vr);
+    float pr[NB][4];
+#pragma unroll
+    for (int nb = 0; nb < NB; nb++) {
+      float4v sc = Tr::qk(kr, q[nb]);
+      float sv[4];
+      float mx = -INFINITY;
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const int tok = tok0 + 4 * g + i;
+        sv[i] = tok <= limit[nb] ? sc[i] * p.scale_log2 : -INFINITY;
+        mx = fmaxf(mx, sv[i]);
+      }
+      mx = wave_max_across_groups(mx);
+      const float m_new = fmaxf(m[nb], mx);
+      const float m_use = m_new == -INFINITY ? 0.f : m_new;
+      const float alpha = exp2f(m[nb] - m_use);
+      float psum = 0.f;
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        pr[nb][i] = exp2f(sv[i] - m_use);
+        psum += pr[nb][i];
+      }
+      lsum[nb] = lsum[nb] * alpha + psum;
+      m[nb] = m_new;
+#pragma unroll
+      for (int n = 0; n < D / 16; n++) o[nb][n] *= alpha;
+    }
+    // V tile written by this wavefront's own lanes: wait for the LDS writes
+    // before the transposed reads of other lanes' rows.
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    Tr::template pv<NB>(lds, l, pr, o);
+  };
+
+  typename Tr::kreg_t ka[Tr::kLoads], kb[Tr::kLoads];
+  typename Tr::vreg_t va[Tr::kLoads], vb[Tr::kLoads];
+  {
+    const int64_t off0 = slab_offset(k0);
+    Tr::load_k(kpool + off0, l, ka);
+    Tr::load_v(vpool + off0, l, va);
+    const int64_t off1 = slab_offset(min(k0 + 1, k1 - 1));
+    Tr::load_k(kpool + off1, l, kb);
+    Tr::load_v(vpool + off1, l, vb);
+  }
+  for (int k = k0; k < k1; k += 2) {
+    process(k, ka, va);
+    {
+      const int64_t off = slab_offset(min(k + 2, k1 - 1));
+      Tr::load_k(kpool + off, l, ka);
+      Tr::load_v(vpool + off, l, va);
+    }
+    if (k + 1 < k1) {
+      process(k + 1, kb, vb);
+      const int64_t off = slab_offset(min(k + 3, k1 - 1));
+      Tr::load_k(kpool + off, l, kb);
+      Tr::load_v(vpool + off, l, vb);
+    }
+  }
+
+#pragma unroll
+  for (int nb = 0; nb < NB; nb++) {
+    const float ltot = wave_sum_across_groups(lsum[nb]);
+    if (n_parts == 1) {
+      if (row_valid[nb]) {
+        const float inv = 1.f / ltot;
+        T* dst = static_cast<T*>(p.out) + (int64_t)q_head[nb] * p.out_stride_head + (int64_t)q_tok[nb] * p.out_stride_token;
+#pragma unroll
+        for (int n = 0; n < D / 16; n++) Tr::store_out(dst + 16 * n + 4 * g, o[nb][n] * inv);
+      }
+    } else {
+      const int64_t prow = unit * kTileRows + nb * 16 + (l & 15);
+      if (row_valid[nb]) {
+        float* dst = p.partial_o + prow * D;
+#pragma unroll
+        for (int n = 0; n < D / 16; n++) *reinterpret_cast<float4v*>(dst + 16 * n + 4 * g) = o[nb][n];
+        if (g == 0) {
+          p.partial_ml[prow * 2 + 0] = m[nb];
+          p.partial_ml[prow * 2 + 1] = ltot;
+        }
+      }
+    }
+  }
+}
+
+// Merges the context partitions of every (b, h, rt) that had more than one.
+// One 256-thread block per (b, h, rt); threads stride over (row, 4 dims).
+template <typename T, int D, int NB>
+__global__ __launch_bounds__(256) void merge_partitions_kernel(PagedAttentionParams p) {
+  constexpr int kTileRows = 16 * NB;
+  const int tile = blockIdx.x;
+  const int rt = tile % p.row_tiles;
+  const int h = (tile / p.row_tiles) % p.num_kv_heads;
+  const int b = tile / (p.row_tiles * p.num_kv_heads);
+  const SeqInfo s = load_seq(p, b);
+  const int rows = p.group_size * s.q_len;
+  const int n_chunks = tile_chunks(s, p.group_size, rt, kTileRows);
+  const int n_parts = (n_chunks + p.chunks_per_part - 1) / p.chunks_per_part;
+  if (n_parts <= 1) return;
+  const int64_t unit0 = (int64_t)tile * p.max_parts;
+  for (int w = threadIdx.x; w < kTileRows * (D / 4); w += blockDim.x) {
+    const int lr = w / (D / 4);
+    const int d4 = (w % (D / 4)) * 4;
+    const int rho = rt * kTileRows + lr;
+    if (rho >= rows) continue;
+    float mmax = -INFINITY;
+    for (int pp = 0; pp < n_parts; pp++) mmax = fmaxf(mmax, p.partial_ml[((unit0 + pp) * kTileRows + lr) * 2]);
+    const float m_use = mmax == -INFINITY ? 0.f : mmax;
+    float4v acc = {0.f, 0.f, 0.f, 0.f};
+    float den = 0.f;
+    for (int pp = 0; pp < n_parts; pp++) {
+      const int64_t prow = (unit0 + pp) * kTileRows + lr;
+      const float wgt = exp2f(p.partial_ml[prow * 2] - m_use);
+      den += wgt * p.partial_ml[prow * 2 + 1];
+      acc += wgt * *reinterpret_cast<const float4v*>(p.partial_o + prow * D + d4);
+    }
+    const int r = rho / s.q_len, i = rho % s.q_len;
+    T* dst = static_cast<T*>(p.out) + (int64_t)(h * p.group_size + r) * p.out_stride_head +
+             (int64_t)(s.q_start + i) * p.out_stride_token + d4;
+    const float inv = 1.f / den;
+#pragma unroll
+    for (int e = 0; e < 4; e++) dst[e] = (T)(acc[e] * inv);
+  }
+}
+
+template <typename Tr, int D, int NB>
+hipError_t launch_typed(const PagedAttentionPlan& plan, const PagedAttentionParams& params, hipStream_t stream) {
+  const int64_t blocks = (plan.num_units + kWavesPerBlock - 1) / kWavesPerBlock;
+  hipLaunchKernelGGL((paged_attention_kernel<Tr, D, NB>), dim3((unsigned)blocks), dim3(kWaveSize * kWavesPerBlock), 0,
+                     stream, params);
+  hipError_t err = hipGetLastError();
+  if (err != hipSuccess || plan.max_parts <= 1) return err;
+  const int tiles = params.num_seqs * params.num_kv_heads * params.row_tiles;
+  hipLaunchKernelGGL((merge_partitions_kernel<typename Tr::elem, D, NB>), dim3(tiles), dim3(256), 0, stream, params);
+  return hipGetLastError();
+}
+
+} // namespace
+
+hipError_t launch_paged_attention(const PagedAttentionPlan& plan, PagedAttentionParams params, hipStream_t stream) {
+  params.chunks_per_part = plan.chunks_per_part;
+  params.max_parts = plan.max_parts;
+  params.row_tiles = plan.row_tiles;
+  params.num_units = plan.num_units;
+#define MVR_DISPATCH(TR, DD, NBV)                                                             \
+  if (plan.head_dim == DD && plan.row_blocks == NBV) return launch_typed<TR<DD>, DD, NBV>(plan, params, stream);
+  if (plan.dtype == 1) {
+    MVR_DISPATCH(F16Traits, 64, 1)
+    MVR_DISPATCH(F16Traits, 64, 2)
+    MVR_DISPATCH(F16Traits, 128, 1)
+    MVR_DISPATCH(F16Traits, 128, 2)
+  } else {
+    MVR_DISPATCH(F32Traits, 64, 1)
+    MVR_DISPATCH(F32Traits, 64, 2)
+    MVR_DISPATCH(F32Traits, 128, 1)
+    MVR_DISPATCH(F32Traits, 128, 2)
+  }
+#undef MVR_DISPATCH
+  return hipErrorInvalidValue;
+}
+
+} // namespace mvr

@@ -1,0 +1,56 @@
+// Internal launch interface between the C ABI (mvr_attn_api.cpp) and the
+// HIP kernels (paged_attention.hip).  Not part of the public ABI.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace mvr {
+
+// Tokens per MFMA chunk: one 16x16 tile of the score matrix per chunk.
+constexpr int kChunkTokens = 16;
+constexpr int kWaveSize = 64;
+constexpr int kWavesPerBlock = 4;
+
+// One launch of the split-context kernel.  A "unit" is the work of one
+// wavefront: (sequence b, kv head h, row tile rt, context partition part).
+// Rows of a kv head are the grouped query rows rho = r*q_len + i (r = query
+// head within the group, i = query position), the order of the reference's
+// grouped matmul (common.rs:846-858).
+struct PagedAttentionParams {
+  const void* q;
+  int64_t q_stride_head, q_stride_token;
+  const void* key_pool;
+  const void* value_pool;
+  const int32_t* block_tables;
+  int32_t block_table_stride;
+  const int32_t* seq_lens;  // may be null: single_seq_len
+  const int32_t* cu_q_lens; // may be null: single_q_len
+  int32_t single_seq_len, single_q_len;
+  void* out;
+  int64_t out_stride_head, out_stride_token;
+  float* partial_o;  // [units][row_tile_rows][head_dim] fp32, unnormalised
+  float* partial_ml; // [units][row_tile_rows][2]: running max (log2 domain), sum
+  int32_t num_seqs, num_kv_heads, group_size, page_size;
+  int32_t chunks_per_part; // 16-token chunks per context partition
+  int32_t max_parts;       // partitions per (sequence, kv head, row tile) in the grid
+  int32_t row_tiles;       // row tiles per (sequence, kv head)
+  int64_t num_units;
+  float scale_log2; // softmax scale * log2(e)
+};
+
+// Grid shape chosen by the host.
+struct PagedAttentionPlan {
+  int dtype;      // 0 f32, 1 f16
+  int head_dim;   // 64 or 128
+  int row_blocks; // 16-row MFMA blocks per wavefront (1 or 2)
+  int row_tiles;
+  int chunks_per_part;
+  int max_parts;
+  int64_t num_units;
+  size_t partial_bytes; // workspace for partials (0 when max_parts == 1)
+};
+
+hipError_t launch_paged_attention(const PagedAttentionPlan& plan, PagedAttentionParams params, hipStream_t stream);
+
+} // namespace mvr

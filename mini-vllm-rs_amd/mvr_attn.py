@@ -1,0 +1,279 @@
+"""Python binding of libmvr_attn.so (C ABI in include/mvr_attn.h).
+
+Mirrors the reference's attention entry points:
+  * paged_attention(...)          batched page-wise attention over one layer's
+                                  packed requests (replaces the per-request
+                                  loop of forward_attention, common.rs:285-327);
+  * forward_paged_attention(...)  one request with a PagedCacheLayout, same
+                                  arguments and errors as forward_paged_attention
+                                  (common.rs:739-817) behind
+                                  forward_cpu_paged_attention (common.rs:426-464).
+Tensors are torch tensors on the GPU; torch supplies device memory and the
+current stream only.  The library must be built (make -C mini-vllm-rs_amd):
+there is no CPU fallback, and a missing library raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import math
+import os
+from dataclasses import dataclass
+from typing import Optional, Sequence
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libmvr_attn.so")
+
+DTYPE_F32, DTYPE_F16 = 0, 1
+
+MVR_OK = 0
+MVR_E_INVALID_ARGUMENT = -1
+MVR_E_UNSUPPORTED = -2
+MVR_E_LENGTH_MISMATCH = -3
+MVR_E_PAGES_UNCOVERED = -4
+MVR_E_PAGE_ID = -5
+MVR_E_WORKSPACE = -6
+MVR_E_HIP = -7
+
+EXPORTED_SYMBOLS = (
+    "mvr_abi_version",
+    "mvr_last_error",
+    "mvr_paged_attention",
+    "mvr_paged_attention_workspace_size",
+    "mvr_paged_attention_validate",
+    "mvr_forward_paged_attention",
+    "mvr_forward_paged_attention_workspace_size",
+)
+
+
+class MvrError(RuntimeError):
+    def __init__(self, code: int, message: str):
+        super().__init__(f"{message} (code {code})")
+        self.code = code
+        self.message = message
+
+
+class PagedAttentionArgs(ctypes.Structure):
+    _fields_ = [
+        ("dtype", ctypes.c_int32),
+        ("num_seqs", ctypes.c_int32),
+        ("num_q_heads", ctypes.c_int32),
+        ("num_kv_heads", ctypes.c_int32),
+        ("head_dim", ctypes.c_int32),
+        ("page_size", ctypes.c_int32),
+        ("num_pages", ctypes.c_int64),
+        ("max_pages_per_seq", ctypes.c_int32),
+        ("max_q_len", ctypes.c_int32),
+        ("max_seq_len", ctypes.c_int32),
+        ("scale", ctypes.c_float),
+        ("q", ctypes.c_void_p),
+        ("q_stride_head", ctypes.c_int64),
+        ("q_stride_token", ctypes.c_int64),
+        ("key_pool", ctypes.c_void_p),
+        ("value_pool", ctypes.c_void_p),
+        ("block_tables", ctypes.c_void_p),
+        ("seq_lens", ctypes.c_void_p),
+        ("cu_q_lens", ctypes.c_void_p),
+        ("out", ctypes.c_void_p),
+        ("out_stride_head", ctypes.c_int64),
+        ("out_stride_token", ctypes.c_int64),
+        ("workspace", ctypes.c_void_p),
+        ("workspace_bytes", ctypes.c_size_t),
+        ("stream", ctypes.c_void_p),
+    ]
+
+
+class AttentionDimensions(ctypes.Structure):
+    _fields_ = [
+        ("num_q_heads", ctypes.c_int32),
+        ("num_kv_heads", ctypes.c_int32),
+        ("head_dim", ctypes.c_int32),
+        ("cached_kv_len", ctypes.c_int32),
+        ("q_len", ctypes.c_int32),
+    ]
+
+
+class PagedCacheLayoutC(ctypes.Structure):
+    _fields_ = [
+        ("key_pool", ctypes.c_void_p),
+        ("value_pool", ctypes.c_void_p),
+        ("page_count", ctypes.c_int64),
+        ("page_ids", ctypes.c_void_p),
+        ("num_page_ids", ctypes.c_int32),
+        ("per_page_token_count", ctypes.c_int32),
+        ("cached_token_count", ctypes.c_int32),
+    ]
+
+
+_lib = None
+
+
+def library_path() -> str:
+    return LIB_PATH
+
+
+def load_library():
+    """Loads libmvr_attn.so from this package directory; raises if it was not built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise RuntimeError(f"{LIB_PATH} is missing: build it with `make -C {HERE}` (no CPU fallback exists)")
+    lib = ctypes.CDLL(LIB_PATH)
+    lib.mvr_abi_version.restype = ctypes.c_int
+    lib.mvr_last_error.restype = ctypes.c_char_p
+    lib.mvr_paged_attention.restype = ctypes.c_int
+    lib.mvr_paged_attention.argtypes = [ctypes.POINTER(PagedAttentionArgs)]
+    lib.mvr_paged_attention_workspace_size.restype = ctypes.c_size_t
+    lib.mvr_paged_attention_workspace_size.argtypes = [ctypes.POINTER(PagedAttentionArgs)]
+    lib.mvr_paged_attention_validate.restype = ctypes.c_int
+    lib.mvr_paged_attention_validate.argtypes = [ctypes.POINTER(PagedAttentionArgs), ctypes.c_void_p,
+                                                 ctypes.c_void_p, ctypes.c_void_p]
+    lib.mvr_forward_paged_attention.restype = ctypes.c_int
+    lib.mvr_forward_paged_attention.argtypes = [ctypes.c_int32, ctypes.POINTER(AttentionDimensions),
+                                                ctypes.POINTER(PagedCacheLayoutC), ctypes.c_void_p, ctypes.c_void_p,
+                                                ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]
+    lib.mvr_forward_paged_attention_workspace_size.restype = ctypes.c_size_t
+    lib.mvr_forward_paged_attention_workspace_size.argtypes = [ctypes.c_int32, ctypes.POINTER(AttentionDimensions),
+                                                               ctypes.POINTER(PagedCacheLayoutC)]
+    if lib.mvr_abi_version() != 1:
+        raise RuntimeError("libmvr_attn.so ABI version mismatch")
+    _lib = lib
+    return lib
+
+
+def _check(rc: int) -> None:
+    if rc != MVR_OK:
+        msg = load_library().mvr_last_error().decode()
+        raise MvrError(rc, msg)
+
+
+def _torch():
+    import torch  # imported lazily: CPU-only users of this module need no torch
+
+    return torch
+
+
+def dtype_code(t) -> int:
+    torch = _torch()
+    if t.dtype == torch.float16:
+        return DTYPE_F16
+    if t.dtype == torch.float32:
+        return DTYPE_F32
+    raise MvrError(MVR_E_UNSUPPORTED, f"activation dtype {t.dtype} is not F32 or F16")
+
+
+def _stream_handle(stream) -> Optional[int]:
+    torch = _torch()
+    if stream is None:
+        stream = torch.cuda.current_stream()
+    return stream.cuda_stream
+
+
+def make_args(q, key_pool, value_pool, block_tables, seq_lens, cu_q_lens, out, *, max_q_len: int,
+              max_seq_len: int, scale: float = 0.0, stream=None) -> PagedAttentionArgs:
+    """Fills the C argument struct.  q / out: [Hq, total_q, D] (last dim contiguous);
+    pools: [num_pages, 1, Hkv, page_size, D]; block_tables int32 [num_seqs, max_pages]."""
+    n_pages, one, hkv, page_size, d = key_pool.shape
+    if one != 1 or value_pool.shape != key_pool.shape:
+        raise MvrError(MVR_E_INVALID_ARGUMENT, "pools must be [num_pages, 1, num_kv_heads, page_size, head_dim]")
+    if q.dim() != 3 or q.stride(2) != 1 or out.dim() != 3 or out.stride(2) != 1:
+        raise MvrError(MVR_E_INVALID_ARGUMENT, "q and out must be [num_q_heads, tokens, head_dim] with unit last stride")
+    if not key_pool.is_contiguous() or not value_pool.is_contiguous() or not block_tables.is_contiguous():
+        raise MvrError(MVR_E_INVALID_ARGUMENT, "pools and block tables must be contiguous")
+    a = PagedAttentionArgs()
+    a.dtype = dtype_code(q)
+    a.num_seqs = block_tables.shape[0]
+    a.num_q_heads = q.shape[0]
+    a.num_kv_heads = hkv
+    a.head_dim = d
+    a.page_size = page_size
+    a.num_pages = n_pages
+    a.max_pages_per_seq = block_tables.shape[1]
+    a.max_q_len = max_q_len
+    a.max_seq_len = max_seq_len
+    a.scale = scale
+    a.q = q.data_ptr()
+    a.q_stride_head = q.stride(0)
+    a.q_stride_token = q.stride(1)
+    a.key_pool = key_pool.data_ptr()
+    a.value_pool = value_pool.data_ptr()
+    a.block_tables = block_tables.data_ptr()
+    a.seq_lens = seq_lens.data_ptr() if seq_lens is not None else None
+    a.cu_q_lens = cu_q_lens.data_ptr() if cu_q_lens is not None else None
+    a.out = out.data_ptr()
+    a.out_stride_head = out.stride(0)
+    a.out_stride_token = out.stride(1)
+    a.stream = _stream_handle(stream)
+    return a
+
+
+def workspace_size(args: PagedAttentionArgs) -> int:
+    return int(load_library().mvr_paged_attention_workspace_size(ctypes.byref(args)))
+
+
+def paged_attention(q, key_pool, value_pool, block_tables, seq_lens, cu_q_lens, out=None, *, max_q_len: int,
+                    max_seq_len: int, scale: float = 0.0, workspace=None, stream=None):
+    """Batched page-wise attention; returns out [Hq, total_q, D] in q's dtype."""
+    torch = _torch()
+    if out is None:
+        out = torch.empty_like(q, memory_format=torch.contiguous_format)
+    a = make_args(q, key_pool, value_pool, block_tables, seq_lens, cu_q_lens, out, max_q_len=max_q_len,
+                  max_seq_len=max_seq_len, scale=scale, stream=stream)
+    need = workspace_size(a)
+    if need and (workspace is None or workspace.numel() * workspace.element_size() < need):
+        workspace = torch.empty(need, dtype=torch.uint8, device=q.device)
+    if workspace is not None:
+        a.workspace = workspace.data_ptr()
+        a.workspace_bytes = workspace.numel() * workspace.element_size()
+    _check(load_library().mvr_paged_attention(ctypes.byref(a)))
+    return out
+
+
+def validate(args: PagedAttentionArgs, block_tables_host=None, seq_lens_host=None, cu_q_lens_host=None) -> None:
+    """Host-side table checks (numpy int32 arrays or None); raises MvrError."""
+    import numpy as np
+
+    def ptr(x):
+        if x is None:
+            return None
+        x = np.ascontiguousarray(x, dtype=np.int32)
+        ptr.keep.append(x)
+        return x.ctypes.data
+
+    ptr.keep = []
+    _check(load_library().mvr_paged_attention_validate(ctypes.byref(args), ptr(block_tables_host),
+                                                      ptr(seq_lens_host), ptr(cu_q_lens_host)))
+
+
+@dataclass
+class PagedCacheLayout:
+    """PagedCacheLayout (src/models/mod.rs:94-100); page_ids live on the device as int32."""
+
+    key_pool: object
+    value_pool: object
+    page_ids: object
+    per_page_token_count: int
+    cached_token_count: int
+
+
+def forward_paged_attention(request_q, layout: PagedCacheLayout, num_q_heads: int, num_kv_heads: int, head_dim: int,
+                            cached_kv_len: int, q_len: int, stream=None):
+    """One request: request_q [1, Hq, q_len, D] -> [1, Hq, q_len, D] (common.rs:739-817)."""
+    torch = _torch()
+    dims = AttentionDimensions(num_q_heads, num_kv_heads, head_dim, cached_kv_len, q_len)
+    c = PagedCacheLayoutC(layout.key_pool.data_ptr(), layout.value_pool.data_ptr(), layout.key_pool.shape[0],
+                          layout.page_ids.data_ptr(), layout.page_ids.numel(), layout.per_page_token_count,
+                          layout.cached_token_count)
+    q = request_q.contiguous()
+    y = torch.empty_like(q)
+    dt = dtype_code(q)
+    lib = load_library()
+    need = int(lib.mvr_forward_paged_attention_workspace_size(dt, ctypes.byref(dims), ctypes.byref(c)))
+    ws = torch.empty(max(need, 1), dtype=torch.uint8, device=q.device)
+    _check(lib.mvr_forward_paged_attention(dt, ctypes.byref(dims), ctypes.byref(c), q.data_ptr(), y.data_ptr(),
+                                           ws.data_ptr(), need, _stream_handle(stream)))
+    return y
+
+
+def pages_for(seq_len: int, page_size: int) -> int:
+    return math.ceil(seq_len / page_size)

@@ -1,0 +1,232 @@
+"""Seeded synthetic page-wise attention workloads.
+
+Five shapes: Qwen2-0.5B decode (F32 and batched F16), Llama-3-8B batch-64 x 8K
+decode, Qwen2-7B chunked prefill and Llama-3-8B speculative verification with
+shared prefix pages.  Block tables, lengths and values are derived from a seed
+so the GPU and the CPU see identical bytes: tables and lengths with numpy's
+PCG64, values either with numpy (host, for parity tests) or torch's device
+generator (fast, for benchmarks).
+
+Layouts follow the reference's data contract (src/models/mod.rs:56-100):
+pools [num_pages, 1, Hkv, page_size, D]; q / out [Hq, total_q, D] (the packed
+[1, Hq, packed_q_len, D] layout of common.rs:268-275); block tables int32
+[num_seqs, max_pages_per_seq]; seq_lens = cached_token_count (current query
+included); cu_q_lens = prefix sums of q_len.
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass, field
+from typing import Dict, List, Optional
+
+import numpy as np
+
+SEED_BASE = 0x6D76720000
+
+
+@dataclass
+class Workload:
+    name: str
+    dtype: str  # "f32" | "f16"
+    num_q_heads: int
+    num_kv_heads: int
+    head_dim: int
+    page_size: int
+    num_pages: int
+    value_scale: float
+    seq_lens: np.ndarray       # int32 [B]
+    q_lens: np.ndarray         # int32 [B]
+    block_tables: np.ndarray   # int32 [B, max_pages]
+    seed: int
+    shared_pages: int = 0      # pages read by more than one sequence (counted once in unique bytes)
+    notes: str = ""
+
+    @property
+    def num_seqs(self) -> int:
+        return len(self.seq_lens)
+
+    @property
+    def cu_q_lens(self) -> np.ndarray:
+        return np.concatenate([[0], np.cumsum(self.q_lens)]).astype(np.int32)
+
+    @property
+    def total_q(self) -> int:
+        return int(self.q_lens.sum())
+
+    @property
+    def elem_size(self) -> int:
+        return 2 if self.dtype == "f16" else 4
+
+    @property
+    def np_dtype(self):
+        return np.float16 if self.dtype == "f16" else np.float32
+
+    @property
+    def max_q_len(self) -> int:
+        return int(self.q_lens.max())
+
+    @property
+    def max_seq_len(self) -> int:
+        return int(self.seq_lens.max())
+
+    def kv_bytes(self) -> int:
+        """Logical K+V bytes one call reads: every visible token of every sequence."""
+        return int(self.seq_lens.sum()) * self.num_kv_heads * self.head_dim * self.elem_size * 2
+
+    def unique_kv_bytes(self) -> int:
+        return self.kv_bytes() - self.shared_pages * self.page_size * self.num_kv_heads * self.head_dim * \
+            self.elem_size * 2
+
+    def algorithmic_bytes(self, unique: bool = False) -> int:
+        """K/V read + Q read + O written + block-table entries read."""
+        kv = self.unique_kv_bytes() if unique else self.kv_bytes()
+        qo = self.total_q * self.num_q_heads * self.head_dim * self.elem_size * 2
+        bt = int(sum(math.ceil(int(L) / self.page_size) for L in self.seq_lens)) * 4
+        return kv + qo + bt
+
+    def flops(self) -> int:
+        """2 flops per multiply-add for QK^T and PV over causally visible (query, key) pairs."""
+        pairs = 0
+        for L, q in zip(self.seq_lens.tolist(), self.q_lens.tolist()):
+            c = L - q
+            pairs += q * c + q * (q + 1) // 2
+        return 4 * pairs * self.num_q_heads * self.head_dim
+
+    def describe(self) -> Dict:
+        return dict(workload=self.name, dtype=self.dtype, num_seqs=self.num_seqs, num_q_heads=self.num_q_heads,
+                    num_kv_heads=self.num_kv_heads, head_dim=self.head_dim, page_size=self.page_size,
+                    num_pages=self.num_pages, total_q=self.total_q, max_seq_len=self.max_seq_len,
+                    sum_seq_len=int(self.seq_lens.sum()), seed=self.seed)
+
+
+def _assign_pages(rng, seq_lens, page_size, num_pages):
+    """Pages for each sequence drawn in order from one shuffle of the pool."""
+    perm = rng.permutation(num_pages).astype(np.int32)
+    need = [math.ceil(int(L) / page_size) for L in seq_lens]
+    if sum(need) > num_pages:
+        raise ValueError("pool too small")
+    bt = np.zeros((len(seq_lens), max(need)), np.int32)
+    used = 0
+    for s, n in enumerate(need):
+        bt[s, :n] = perm[used:used + n]
+        used += n
+    return bt
+
+
+def qwen2_05b_decode_f32() -> Workload:
+    """1 sequence, 1 query token, 14 Q / 2 KV heads, D 64, 512 tokens in 16-token pages, pool 64 pages."""
+    seed = SEED_BASE + 1
+    rng = np.random.default_rng(seed)
+    perm = rng.permutation(64).astype(np.int32)
+    return Workload("qwen2-0.5b decode f32 b1 ctx512", "f32", 14, 2, 64, 16, 64, 0.5,
+                    np.array([512], np.int32), np.array([1], np.int32), perm[None, :32].copy(), seed)
+
+
+def qwen2_05b_batched_decode_f16() -> Workload:
+    """Batch 8, lengths U[128, 4096], 14 Q / 2 KV, D 64, pool of 4096 pages."""
+    seed = SEED_BASE + 2
+    rng = np.random.default_rng(seed)
+    seq_lens = rng.integers(128, 4096, size=8, endpoint=True).astype(np.int32)
+    bt = _assign_pages(rng, seq_lens, 16, 4096)
+    return Workload("qwen2-0.5b decode f16 b8 ctxU[128,4096]", "f16", 14, 2, 64, 16, 4096, 0.5, seq_lens,
+                    np.ones(8, np.int32), bt, seed)
+
+
+def llama3_8b_decode_b64_8k_f16(batch: int = 64) -> Workload:
+    """Batch 64 x 8192 tokens, 32 Q / 8 KV, D 128, pool = exact fit (32768 pages), permuted."""
+    seed = SEED_BASE + 3
+    rng = np.random.default_rng(seed)
+    seq_lens = np.full(batch, 8192, np.int32)
+    num_pages = batch * 512
+    bt = _assign_pages(rng, seq_lens, 16, num_pages)
+    return Workload(f"llama3-8b decode f16 b{batch} ctx8192", "f16", 32, 8, 128, 16, num_pages, 0.3, seq_lens,
+                    np.ones(batch, np.int32), bt, seed)
+
+
+def qwen2_7b_chunked_prefill_f16() -> Workload:
+    """4 sequences, 2048 cached + 256 new tokens, 28 Q / 4 KV, D 128, pages in random order."""
+    seed = SEED_BASE + 4
+    rng = np.random.default_rng(seed)
+    seq_lens = np.full(4, 2048 + 256, np.int32)
+    num_pages = 4 * math.ceil(2304 / 16)
+    bt = _assign_pages(rng, seq_lens, 16, num_pages)
+    return Workload("qwen2-7b chunked prefill f16 b4 2048+256", "f16", 28, 4, 128, 16, num_pages, 0.3, seq_lens,
+                    np.full(4, 256, np.int32), bt, seed)
+
+
+def llama3_8b_spec_verify_f16() -> Workload:
+    """16 sequences verifying 5 positions; contexts U[1024, 16384]; groups of 4 share the first 1024 tokens' pages."""
+    seed = SEED_BASE + 5
+    rng = np.random.default_rng(seed)
+    ctx = rng.integers(1024, 16384, size=16, endpoint=True).astype(np.int32)
+    q = 5
+    seq_lens = (ctx + q).astype(np.int32)
+    shared = 1024 // 16
+    private = [math.ceil(int(L) / 16) - shared for L in seq_lens]
+    num_pages = 4 * shared + sum(private)
+    perm = rng.permutation(num_pages).astype(np.int32)
+    bt = np.zeros((16, max(p + shared for p in private)), np.int32)
+    used = 0
+    group_prefix = []
+    for grp in range(4):
+        group_prefix.append(perm[used:used + shared])
+        used += shared
+    for s in range(16):
+        bt[s, :shared] = group_prefix[s // 4]
+        bt[s, shared:shared + private[s]] = perm[used:used + private[s]]
+        used += private[s]
+    # Each group's prefix pages are read by 4 sequences; 3 of the 4 reads are repeats.
+    return Workload("llama3-8b spec-verify f16 b16 q5 ctxU[1024,16384] shared-prefix", "f16", 32, 8, 128, 16,
+                    num_pages, 0.3, seq_lens, np.full(16, q, np.int32), bt, seed, shared_pages=12 * shared)
+
+
+CONFIGS = {
+    1: qwen2_05b_decode_f32,
+    2: qwen2_05b_batched_decode_f16,
+    3: llama3_8b_decode_b64_8k_f16,
+    4: qwen2_7b_chunked_prefill_f16,
+    5: llama3_8b_spec_verify_f16,
+}
+
+
+def host_values(w: Workload, chunk: int = 1 << 26):
+    """(q, key_pool, value_pool) as numpy arrays in the workload dtype, N(0,1)*scale, from numpy's PCG64."""
+    rng = np.random.default_rng(w.seed ^ 0x5EED)
+    shape_pool = (w.num_pages, 1, w.num_kv_heads, w.page_size, w.head_dim)
+
+    def normal(shape):
+        out = np.empty(shape, w.np_dtype)
+        flat = out.reshape(-1)
+        for s in range(0, flat.size, chunk):
+            n = min(chunk, flat.size - s)
+            flat[s:s + n] = (rng.standard_normal(n, dtype=np.float32) * np.float32(w.value_scale)).astype(w.np_dtype)
+        return out
+
+    q = normal((w.num_q_heads, w.total_q, w.head_dim))
+    k = normal(shape_pool)
+    v = normal(shape_pool)
+    return q, k, v
+
+
+def device_tensors(w: Workload, values: Optional[tuple] = None, device: str = "cuda", seed: Optional[int] = None):
+    """Torch tensors on the device.  values=None draws them on the device with torch's generator."""
+    import torch
+
+    tdt = torch.float16 if w.dtype == "f16" else torch.float32
+    if values is None:
+        g = torch.Generator(device=device)
+        g.manual_seed(w.seed if seed is None else seed)
+        shape_pool = (w.num_pages, 1, w.num_kv_heads, w.page_size, w.head_dim)
+
+        def normal(shape):
+            t = torch.empty(shape, dtype=tdt, device=device)
+            t.normal_(0.0, w.value_scale, generator=g)
+            return t
+
+        q, k, v = normal((w.num_q_heads, w.total_q, w.head_dim)), normal(shape_pool), normal(shape_pool)
+    else:
+        q, k, v = (torch.from_numpy(np.ascontiguousarray(x)).to(device) for x in values)
+    bt = torch.from_numpy(w.block_tables).to(device)
+    sl = torch.from_numpy(w.seq_lens).to(device)
+    cu = torch.from_numpy(w.cu_q_lens).to(device)
+    return dict(q=q, key_pool=k, value_pool=v, block_tables=bt, seq_lens=sl, cu_q_lens=cu)

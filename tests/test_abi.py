@@ -1,0 +1,154 @@
+"""CPU-side checks of the C ABI: the library loads, exports every function
+include/mvr_attn.h declares, and its host checks reject bad arguments with
+the reference's errors (common.rs:447-454, :776-781) before any launch."""
+import ctypes
+import os
+import re
+import subprocess
+
+import pytest
+
+import mvr_attn as M
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "mvr_attn.h")
+
+
+def header_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(mvr_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = M.load_library()
+    declared = header_functions()
+    assert declared, "no functions parsed from the header"
+    assert set(declared) == set(M.EXPORTED_SYMBOLS)
+    for name in declared:
+        assert hasattr(lib, name), name
+    out = subprocess.run(["nm", "-D", "--defined-only", M.library_path()], capture_output=True, text=True, check=True)
+    exported = set(re.findall(r"\bT (mvr_[a-z0-9_]+)$", out.stdout, flags=re.M))
+    assert set(declared) <= exported
+    assert M.load_library().mvr_abi_version() == 1
+
+
+def test_product_library_does_not_link_the_oracle():
+    out = subprocess.run(["nm", "-D", M.library_path()], capture_output=True, text=True, check=True).stdout
+    assert "oracle_" not in out
+    ldd = subprocess.run(["ldd", M.library_path()], capture_output=True, text=True).stdout
+    assert "liboracle" not in ldd
+
+
+def _args(**kw):
+    a = M.PagedAttentionArgs()
+    a.dtype = M.DTYPE_F16
+    a.num_seqs = 2
+    a.num_q_heads = 32
+    a.num_kv_heads = 8
+    a.head_dim = 128
+    a.page_size = 16
+    a.num_pages = 1024
+    a.max_pages_per_seq = 64
+    a.max_q_len = 1
+    a.max_seq_len = 1024
+    fake = 1 << 20  # aligned dummy addresses: these calls never launch
+    a.q = a.key_pool = a.value_pool = a.block_tables = a.seq_lens = a.cu_q_lens = a.out = fake
+    a.q_stride_head = 2 * 128
+    a.q_stride_token = 128
+    a.out_stride_head = 2 * 128
+    a.out_stride_token = 128
+    for k, v in kw.items():
+        setattr(a, k, v)
+    return a
+
+
+def _call(a):
+    lib = M.load_library()
+    rc = lib.mvr_paged_attention(ctypes.byref(a))
+    return rc, lib.mvr_last_error().decode()
+
+
+@pytest.mark.parametrize("field,value,code,msg", [
+    ("dtype", 7, M.MVR_E_UNSUPPORTED, "dtype"),
+    ("num_seqs", 0, M.MVR_E_INVALID_ARGUMENT, "forward requires at least one request"),
+    ("num_kv_heads", 5, M.MVR_E_INVALID_ARGUMENT, "not a multiple"),
+    ("head_dim", 96, M.MVR_E_UNSUPPORTED, "head_dim"),
+    ("page_size", 24, M.MVR_E_UNSUPPORTED, "page_size"),
+    ("max_q_len", 0, M.MVR_E_INVALID_ARGUMENT, "at least one token"),
+    ("max_pages_per_seq", 60, M.MVR_E_PAGES_UNCOVERED, "leaving 64 tokens uncovered"),
+    ("q", 1 + (1 << 20), M.MVR_E_INVALID_ARGUMENT, "aligned"),
+    ("q_stride_token", 100, M.MVR_E_INVALID_ARGUMENT, "aligned"),
+    ("seq_lens", None, M.MVR_E_INVALID_ARGUMENT, "required"),
+])
+def test_scalar_checks_reject_before_launch(field, value, code, msg):
+    rc, err = _call(_args(**{field: value}))
+    assert rc == code
+    assert msg in err
+
+
+def test_workspace_too_small_is_rejected():
+    a = _args(max_seq_len=1024)
+    need = M.workspace_size(a)
+    assert need > 0  # 2 sequences x 8 kv heads cannot fill the GPU without splitting the context
+    a.workspace = 1 << 20
+    a.workspace_bytes = need - 1
+    rc, err = _call(a)
+    assert rc == M.MVR_E_WORKSPACE and "smaller than" in err
+
+
+def test_validate_mirrors_reference_errors():
+    a = _args()
+    bt = [[i for i in range(64)], [64 + i for i in range(64)]]
+    M.validate(a, bt, [1024, 17], [0, 1, 2])
+    with pytest.raises(M.MvrError, match="outside a pool of 1024 pages") as e:
+        M.validate(a, [[5000] * 64, bt[1]], [1024, 17], [0, 1, 2])
+    assert e.value.code == M.MVR_E_PAGE_ID
+    with pytest.raises(M.MvrError, match="reports sequence length 0") as e:
+        M.validate(_args(max_q_len=2), bt, [0, 17], [0, 2, 3])
+    assert e.value.code == M.MVR_E_LENGTH_MISMATCH
+    with pytest.raises(M.MvrError, match="at least one token"):
+        M.validate(a, bt, [1024, 17], [0, 0, 1])
+    with pytest.raises(M.MvrError, match="max_seq_len"):
+        M.validate(a, bt, [2000, 17], [0, 1, 2])
+
+
+def test_request_level_entry_checks_lengths():
+    lib = M.load_library()
+    dims = M.AttentionDimensions(14, 2, 64, 511, 1)
+    lay = M.PagedCacheLayoutC(1 << 20, 1 << 20, 64, 1 << 20, 32, 16, 513)
+    rc = lib.mvr_forward_paged_attention(M.DTYPE_F32, ctypes.byref(dims), ctypes.byref(lay), 1 << 20, 1 << 20, None, 0,
+                                         None)
+    assert rc == M.MVR_E_LENGTH_MISMATCH
+    assert "paged KV cache reports sequence length 513, expected 512" in lib.mvr_last_error().decode()
+    lay = M.PagedCacheLayoutC(1 << 20, 1 << 20, 64, 1 << 20, 31, 16, 512)
+    rc = lib.mvr_forward_paged_attention(M.DTYPE_F32, ctypes.byref(dims), ctypes.byref(lay), 1 << 20, 1 << 20, None, 0,
+                                         None)
+    assert rc == M.MVR_E_PAGES_UNCOVERED
+    assert "leaving 16 tokens uncovered" in lib.mvr_last_error().decode()
+
+
+def test_workloads_match_stated_sizes():
+    import workloads as W
+
+    w3 = W.llama3_8b_decode_b64_8k_f16()
+    assert w3.algorithmic_bytes() == 2_148_663_296
+    assert w3.kv_bytes() == 2_147_483_648
+    w4 = W.qwen2_7b_chunked_prefill_f16()
+    assert w4.flops() == 31_951_159_296
+    assert w4.kv_bytes() + 2 * 28 * 1024 * 128 * 2 == 33_554_432
+    w1 = W.qwen2_05b_decode_f32()
+    assert w1.kv_bytes() == 524_288
+    w5 = W.llama3_8b_spec_verify_f16()
+    assert w5.kv_bytes() - w5.unique_kv_bytes() == 50_331_648
+    # shared prefixes: 4 groups, identical physical ids inside a group, disjoint elsewhere
+    bt = w5.block_tables
+    for s in range(16):
+        assert (bt[s, :64] == bt[(s // 4) * 4, :64]).all()
+    used = set()
+    for s in range(16):
+        n = -(-int(w5.seq_lens[s]) // 16)
+        ids = bt[s, 64 if s % 4 else 0:n].tolist()
+        assert not used.intersection(ids)
+        used.update(ids)
+    assert len(used) == w5.num_pages

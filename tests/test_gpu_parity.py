@@ -1,0 +1,230 @@
+"""GPU parity: the HIP path (through the C ABI) against the oracle.
+
+Bar: max-abs 1e-5 for F32 and 2e-3 for F16 against the oracle's reference
+dataflow (common.rs:739-817, per-op dtype rounding); page-table indexing
+bit-exact.  Full-size workloads are also checked through size-independent
+properties (block-table relocation, poisoned unused slots, determinism).
+"""
+import json
+import math
+import os
+import sys
+
+import numpy as np
+import pytest
+
+torch = pytest.importorskip("torch")
+
+import mvr_attn as M  # noqa: E402
+import oracle as O  # noqa: E402
+import workloads as W  # noqa: E402
+
+pytestmark = pytest.mark.gpu
+
+TOL = {"f32": 1e-5, "f16": 2e-3}
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden", "reference_kats.json")
+
+
+def say(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _gpu():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    M.load_library()
+    O.build()
+
+
+def run_hip(w, t, scale=0.0):
+    out = M.paged_attention(t["q"], t["key_pool"], t["value_pool"], t["block_tables"], t["seq_lens"], t["cu_q_lens"],
+                            max_q_len=w.max_q_len, max_seq_len=w.max_seq_len, scale=scale)
+    torch.cuda.synchronize()
+    return out
+
+
+def run_oracle(w, vals, mode=O.REF_CONCAT_V):
+    q, k, v = vals
+    return O.paged_attention(q, k, v, w.block_tables, w.seq_lens, w.cu_q_lens, w.num_q_heads, w.num_kv_heads,
+                             w.head_dim, w.page_size, dtype=O.F16 if w.dtype == "f16" else O.F32, mode=mode,
+                             num_threads=16)
+
+
+@pytest.mark.parametrize("cfg", [1, 2, 3, 4, 5])
+def test_workload_parity_with_oracle(cfg):
+    w = W.CONFIGS[cfg]()
+    say(f"[parity] config {cfg}: {w.name}")
+    vals = W.host_values(w)
+    t = W.device_tensors(w, vals)
+    out = run_hip(w, t).float().cpu().numpy().astype(np.float64)
+    ref = run_oracle(w, vals)
+    err = np.abs(out - ref).max()
+    exact = run_oracle(w, vals, O.EXACT_F64)
+    err_exact = np.abs(out - exact).max()
+    say(f"[parity] config {cfg}: max-abs vs oracle {err:.3e}, vs f64 {err_exact:.3e}")
+    assert np.isfinite(out).all()
+    assert err <= TOL[w.dtype], err
+
+
+def test_reference_unit_tests_on_gpu():
+    """common.rs:1031-1141 closed forms, head_dim zero-padded to 64 (zeros add nothing to q.k and give zero output
+    columns), keys in 16-token pages with a reversed block table."""
+    cases = json.load(open(GOLDEN))["cases"]
+    for case in cases:
+        if "paged" in case:
+            continue
+        hq, hkv, d = case["num_q_heads"], case["num_kv_heads"], case["head_dim"]
+        c, ql = case["cached_kv_len"], case["q_len"]
+        L = c + ql
+        dt = torch.float16 if case["dtype"] == "f16" else torch.float32
+        D = 64
+        q = torch.zeros(hq, ql, D, dtype=dt)
+        q[:, :, :d] = torch.tensor(case["q"], dtype=torch.float32).reshape(hq, ql, d).to(dt)
+        npages = 3
+        kp = torch.zeros(npages, 1, hkv, 16, D, dtype=dt)
+        vp = torch.zeros(npages, 1, hkv, 16, D, dtype=dt)
+        kk = torch.tensor(case["k"], dtype=torch.float32).reshape(hkv, L, d)
+        vv = torch.tensor(case["v"], dtype=torch.float32).reshape(hkv, L, d)
+        kp[2, 0, :, :L, :d] = kk.to(dt)
+        vp[2, 0, :, :L, :d] = vv.to(dt)
+        bt = torch.tensor([[2, 0]], dtype=torch.int32)
+        out = M.paged_attention(q.cuda(), kp.cuda(), vp.cuda(), bt.cuda(), torch.tensor([L], dtype=torch.int32).cuda(),
+                                torch.tensor([0, ql], dtype=torch.int32).cuda(), max_q_len=ql, max_seq_len=L)
+        torch.cuda.synchronize()
+        got = out.float().cpu()
+        np.testing.assert_allclose(got[:, :, :d].reshape(-1).numpy(), case["expected"], atol=1e-5, rtol=0,
+                                   err_msg=case["name"])
+        assert (got[:, :, d:] == 0).all()
+        assert out.dtype == dt  # common.rs:1095-1123: dtype preserved
+
+
+@pytest.mark.parametrize("dtype", ["f32", "f16"])
+def test_reference_paged_fixture_semantics_on_gpu(dtype):
+    """common.rs:1143-1203 at page size 16: the 5 fixture tokens sit in physical page 2 (block table [2, 0]), the
+    slots past them hold poison 99 and the pages off the table hold 88; GQA 2:1, cached_kv_len 3, q_len 2.
+    F32 must reproduce the fixture's expected output; F16 (inputs rounded to f16) the oracle's."""
+    case = [c for c in json.load(open(GOLDEN))["cases"] if "paged" in c][0]
+    dt = torch.float16 if dtype == "f16" else torch.float32
+    D, P = 64, 16
+    kp = np.full((3, 1, 1, P, D), 88.0, np.float32)
+    vp = np.full((3, 1, 1, P, D), 88.0, np.float32)
+    kp[2], vp[2] = 0.0, 0.0
+    kp[2, 0, 0, 5:], vp[2, 0, 0, 5:] = 99.0, 99.0
+    kp[2, 0, 0, :5, :2] = np.array(case["k"], np.float32).reshape(5, 2)
+    vp[2, 0, 0, :5, :2] = np.array(case["v"], np.float32).reshape(5, 2)
+    q = np.zeros((2, 2, D), np.float32)
+    q[:, :, :2] = np.array(case["q"], np.float32).reshape(2, 2, 2)
+    bt = np.array([[2, 0]], np.int32)
+    out = M.paged_attention(torch.from_numpy(q).to(dt).cuda(), torch.from_numpy(kp).to(dt).cuda(),
+                            torch.from_numpy(vp).to(dt).cuda(), torch.from_numpy(bt).cuda(),
+                            torch.tensor([5], dtype=torch.int32).cuda(), torch.tensor([0, 2], dtype=torch.int32).cuda(),
+                            max_q_len=2, max_seq_len=5, scale=1.0 / math.sqrt(2.0))  # the fixture's head_dim is 2
+    torch.cuda.synchronize()
+    got = out.float().cpu().numpy()
+    assert (got[:, :, 2:] == 0).all()
+    if dtype == "f32":
+        np.testing.assert_allclose(got[:, :, :2].reshape(-1), case["expected"], atol=1e-5, rtol=0)
+    else:
+        args = (q[None, :, :, :2].astype(np.float16), kp[..., :2].astype(np.float16), vp[..., :2].astype(np.float16),
+                [2], P, 5, 2, 1, 2, 3, 2)
+        ref = O.forward_paged_attention(*args, dtype=O.F16)
+        exact = O.forward_paged_attention(*args, dtype=O.F16, mode=O.EXACT_F64)
+        # Outputs here are 4..6, where one f16 ulp is 3.9e-3: the 2e-3 bar scales with |output| above 1.
+        np.testing.assert_allclose(got[:, :, :2], ref, atol=2e-3, rtol=2e-3)
+        # fp32 accumulation then one rounding: within half an f16 ulp of the exact answer (plus fp32 noise).
+        half_ulp = np.spacing(np.abs(exact).astype(np.float16)).astype(np.float64) / 2
+        assert (np.abs(got[:, :, :2] - exact) <= half_ulp + 1e-5).all()
+
+
+def test_request_level_entry_matches_batched():
+    w = W.qwen2_05b_batched_decode_f16()
+    vals = W.host_values(w)
+    t = W.device_tensors(w, vals)
+    batched = run_hip(w, t)
+    for s in range(w.num_seqs):
+        L = int(w.seq_lens[s])
+        n = math.ceil(L / w.page_size)
+        lay = M.PagedCacheLayout(t["key_pool"], t["value_pool"], t["block_tables"][s, :n].contiguous(), w.page_size, L)
+        rq = t["q"][:, s:s + 1].unsqueeze(0)
+        y = M.forward_paged_attention(rq, lay, w.num_q_heads, w.num_kv_heads, w.head_dim, L - 1, 1)
+        torch.cuda.synchronize()
+        assert torch.equal(y[0], batched[:, s:s + 1])
+
+
+def test_one_hot_gather_is_bit_exact():
+    """Page-table indexing: each query row's softmax is one-hot on a chosen logical key, so the output must equal
+    that key's V row bit for bit (V rows encode page, slot, head and dim as exact integers)."""
+    rng = np.random.default_rng(21)
+    for dtype in ("f16", "f32"):
+        hq, hkv, D, P, N = 8, 2, 64, 16, 40
+        seq_lens = np.array([37, 300, 129], np.int32)
+        bt = np.zeros((3, 20), np.int32)
+        perm = rng.permutation(N)
+        used = 0
+        for s, L in enumerate(seq_lens):
+            n = math.ceil(L / P)
+            bt[s, :n] = perm[used:used + n]
+            used += n
+        kp = np.zeros((N, 1, hkv, P, D), np.float32)
+        vp = np.zeros((N, 1, hkv, P, D), np.float32)
+        pg, hh, tt, dd = np.meshgrid(np.arange(N), np.arange(hkv), np.arange(P), np.arange(D), indexing="ij")
+        vp[:, 0] = (pg * 7 + tt * 3 + hh * 5 + dd) % 1000  # exact in f16
+        q = np.zeros((hq, 3, D), np.float32)
+        targets = {}
+        for s, L in enumerate(seq_lens):
+            for h in range(hq):
+                j = int(rng.integers(0, L))
+                targets[(s, h)] = j
+                kvh = h // (hq // hkv)
+                e = np.zeros(D, np.float32)
+                e[h % (hq // hkv) + 4 * s] = 16.0  # distinct direction per (sequence, query head in group)
+                kp[bt[s, j // P], 0, kvh, j % P] += e
+                q[h, s] = e
+        dt = torch.float16 if dtype == "f16" else torch.float32
+        out = M.paged_attention(torch.from_numpy(q).to(dt).cuda(), torch.from_numpy(kp).to(dt).cuda(),
+                                torch.from_numpy(vp).to(dt).cuda(), torch.from_numpy(bt).cuda(),
+                                torch.from_numpy(seq_lens).cuda(), torch.tensor([0, 1, 2, 3], dtype=torch.int32).cuda(),
+                                max_q_len=1, max_seq_len=300, scale=1.0)
+        torch.cuda.synchronize()
+        got = out.float().cpu().numpy()
+        for (s, h), j in targets.items():
+            want = vp[bt[s, j // P], 0, h // (hq // hkv), j % P]
+            assert np.array_equal(got[h, s], want), (dtype, s, h, j)
+
+
+def test_full_size_properties_decode_b64():
+    """Llama-3-8B batch 64 x 8K: relocating every page (and the table with it) and poisoning pages off the table
+    leave the output bit-identical; two runs are bit-identical."""
+    w = W.llama3_8b_decode_b64_8k_f16()
+    say("[props] config 3 full size")
+    t = W.device_tensors(w, None)
+    a = run_hip(w, t).clone()
+    b = run_hip(w, t)
+    assert torch.equal(a, b)
+    perm = torch.randperm(w.num_pages, generator=torch.Generator().manual_seed(5)).to(torch.int32).cuda()
+    k2 = torch.empty_like(t["key_pool"])
+    v2 = torch.empty_like(t["value_pool"])
+    k2[perm.long()] = t["key_pool"]
+    v2[perm.long()] = t["value_pool"]
+    del t["key_pool"], t["value_pool"]
+    t2 = dict(t, key_pool=k2, value_pool=v2, block_tables=perm[t["block_tables"].long()].contiguous())
+    c = run_hip(w, t2)
+    assert torch.equal(a, c)
+
+
+def test_poisoned_tail_slots_and_foreign_pages_are_ignored():
+    """Slots past each sequence's length and pages of no table hold NaN/Inf; outputs are unchanged bit for bit."""
+    w = W.llama3_8b_spec_verify_f16()
+    vals = W.host_values(w)
+    t = W.device_tensors(w, vals)
+    a = run_hip(w, t).clone()
+    k, v = vals[1].copy(), vals[2].copy()
+    for s, L in enumerate(w.seq_lens.tolist()):
+        last = w.block_tables[s, (L - 1) // w.page_size]
+        k[last, 0, :, (L - 1) % w.page_size + 1:] = np.nan
+        v[last, 0, :, (L - 1) % w.page_size + 1:] = np.inf
+    t2 = W.device_tensors(w, (vals[0], k, v))
+    b = run_hip(w, t2)
+    assert torch.equal(a, b)
