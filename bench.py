@@ -20,7 +20,9 @@ sys.path.insert(0, os.path.join(ROOT, "mini-vllm-rs_amd"))
 
 HBM_PEAK_GBS = 8000.0      # MI355X HBM3E, 8 TB/s
 MFMA_F16_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 MFMA
-TRAFFIC_FILE = os.path.join(ROOT, "profiles", "hbm_traffic.json")
+# HBM bytes per launch of the split-context kernel, from the FETCH_SIZE / WRITE_SIZE counter runs
+# summarised in this file (line "bytes_per_launch: N").
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "paged_attention_decode_b64_ctx8192_f16_hbm_traffic.md")
 
 
 def log(msg):
@@ -38,7 +40,7 @@ class Runner:
                                 tensors["seq_lens"], tensors["cu_q_lens"], self.out, max_q_len=w.max_q_len,
                                 max_seq_len=w.max_seq_len)
         need = M.workspace_size(self.args)
-        self.ws = torch.empty(max(need, 256), dtype=torch.uint8, device="cuda")
+        self.ws = M.new_workspace(need, "cuda")
         self.args.workspace = self.ws.data_ptr()
         self.args.workspace_bytes = need
         self.lib = M.load_library()
@@ -134,6 +136,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--skip-cpu", action="store_true")
     ap.add_argument("--only-headline", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="also run 3 device copies of 1 GiB (a plain copy kernel of known size, for HBM counters)")
     a = ap.parse_args()
     if a.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {a.gpus} is not supported (this path is single-GPU; "
@@ -162,11 +166,21 @@ def main():
     log(f"[bench] headline median {med:.1f} us, mean {mean:.1f} us, {value:.0f} GB/s")
     del t, r
     torch.cuda.empty_cache()
+    if a.copy_calibration:
+        src = torch.empty(1 << 30, dtype=torch.uint8, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
+        torch.cuda.empty_cache()
 
     traffic = None
     if os.path.exists(TRAFFIC_FILE):
         with open(TRAFFIC_FILE) as f:
-            traffic = json.load(f).get("bytes_per_launch")
+            for line in f:
+                if line.startswith("bytes_per_launch:"):
+                    traffic = int(line.split(":")[1])
 
     result = {
         "metric": "decode attention us/step + effective KV-read GB/s (% HBM peak), 1 MI355X",
@@ -192,7 +206,9 @@ def main():
             "unit": "GB/s",
             "frac": round(value / HBM_PEAK_GBS, 4),
             "traffic": traffic,
-            "timed": "whole attention call (split-context kernel + partition merge), HIP events on the launch stream",
+            "timed": "mean duration of the whole attention call (paged_attention_kernel + merge_partitions_kernel) "
+                     "between HIP events recorded on the launch stream; the rocprofv3 kernel-trace summary in "
+                     "profiles/ lists both kernels' averages, whose sum this mean should match",
         },
     }
     if not a.only_headline:

@@ -92,7 +92,10 @@ typedef struct mvr_paged_attention_args {
 } mvr_paged_attention_args;
 
 /* Bytes of workspace mvr_paged_attention needs for these arguments (depends
-   only on the scalar fields).  May be 0. */
+   only on the scalar fields; 0 when no sequence is split into context
+   partitions).  The workspace holds fp32 partial results of the partitions;
+   its contents need no initialisation and are dead after the call.  Calls
+   that share a workspace must not overlap in time. */
 size_t mvr_paged_attention_workspace_size(const mvr_paged_attention_args* args);
 
 /* Batched page-wise attention (decode, speculative verification and chunked

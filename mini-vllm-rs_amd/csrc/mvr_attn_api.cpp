@@ -39,9 +39,8 @@ int chunks_per_partition_override() {
   return v;
 }
 
-int target_waves() {
-  // 256 CUs x 16 resident wavefronts is the fill target on MI355X.
-  static const int v = env_int("MVR_ATTN_TARGET_WAVES", 256 * 16);
+int target_waves_override() {
+  static const int v = env_int("MVR_ATTN_TARGET_WAVES", 0);
   return v;
 }
 
@@ -98,7 +97,13 @@ mvr::PagedAttentionPlan make_plan(const mvr_paged_attention_args* a) {
   const int64_t base_units = (int64_t)a->num_seqs * a->num_kv_heads * plan.row_tiles;
   int cpp = chunks_per_partition_override();
   if (cpp <= 0) {
-    int64_t parts = (target_waves() + base_units - 1) / base_units;
+    // Split contexts so that the units fill the resident wavefront slots of
+    // the device once: more partitions add merge traffic and a tail round,
+    // fewer leave CUs idle.
+    int64_t slots = target_waves_override();
+    if (slots <= 0) slots = mvr::paged_attention_resident_waves(plan.dtype, plan.head_dim, plan.row_blocks);
+    if (slots <= 0) slots = 256 * 8; // no device to ask (sizing only)
+    int64_t parts = slots / base_units;
     if (parts < 1) parts = 1;
     cpp = (int)((max_chunks + parts - 1) / parts);
     if (cpp < 8) cpp = 8; // at least 128 tokens per wavefront
@@ -109,6 +114,7 @@ mvr::PagedAttentionPlan make_plan(const mvr_paged_attention_args* a) {
   plan.num_units = base_units * plan.max_parts;
   plan.partial_bytes = 0;
   if (plan.max_parts > 1) {
+    // [partial o][partial m, l]
     const size_t prow = (size_t)plan.num_units * tile_rows;
     plan.partial_bytes = align_up(prow * a->head_dim * sizeof(float), 256) + align_up(prow * 2 * sizeof(float), 256);
   }
@@ -156,9 +162,9 @@ int mvr_paged_attention(const mvr_paged_attention_args* a) {
   p.out_stride_token = a->out_stride_token;
   if (plan.partial_bytes) {
     const size_t prow = (size_t)plan.num_units * 16 * plan.row_blocks;
-    p.partial_o = static_cast<float*>(a->workspace);
-    p.partial_ml = reinterpret_cast<float*>(static_cast<char*>(a->workspace) +
-                                            align_up(prow * a->head_dim * sizeof(float), 256));
+    char* ws = static_cast<char*>(a->workspace);
+    p.partial_o = reinterpret_cast<float*>(ws);
+    p.partial_ml = reinterpret_cast<float*>(ws + align_up(prow * a->head_dim * sizeof(float), 256));
   }
   p.num_seqs = a->num_seqs;
   p.num_kv_heads = a->num_kv_heads;

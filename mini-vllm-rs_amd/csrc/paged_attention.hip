@@ -95,6 +95,10 @@ struct F16Traits {
   typedef half8 vreg_t;
   typedef half8 qreg_t;
 
+  // 16-row tiles: 3 wavefronts per SIMD; 32-row tiles: 2.
+  template <int NB>
+  static constexpr int min_blocks() { return NB == 1 ? 3 : 2; }
+
   // 32-byte pieces of an LDS row: D/16; XOR swizzle spreads 16 rows over banks.
   __device__ static __forceinline__ int swz(int t) { return D == 128 ? (t & 7) : ((t >> 1) & 3); }
 
@@ -172,6 +176,9 @@ struct F32Traits {
   typedef float4v vreg_t;
   typedef float4v qreg_t;
 
+  template <int NB>
+  static constexpr int min_blocks() { return D == 128 ? (NB == 1 ? 2 : 1) : (NB == 1 ? 3 : 2); }
+
   // 64-byte pieces (16 floats) of an LDS row; rows 4g+j of the four lane
   // groups land in four different pieces.
   __device__ static __forceinline__ int swz(int t) { return (t >> 2) & 3; }
@@ -233,11 +240,48 @@ struct F32Traits {
   __device__ static __forceinline__ void store_out(float* dst, float4v v) { *reinterpret_cast<float4v*>(dst) = v; }
 };
 
+// Merges the n_parts partial results of tile (b, h, rt) and writes the
+// normalised output: out = sum_p 2^(m_p - M) o_p / sum_p 2^(m_p - M) l_p.
+// Executed by `lanes` threads with ids lane0 .. lane0+lanes-1.
+template <typename T, int D, int NB>
+__device__ __forceinline__ void merge_tile(const PagedAttentionParams& p, int64_t tile, int rt, int h, const SeqInfo& s,
+                                           int n_parts, int lane0, int lanes) {
+  constexpr int kTileRows = 16 * NB;
+  const int rows = p.group_size * s.q_len;
+  const int64_t unit0 = tile * p.max_parts;
+  for (int w = lane0; w < kTileRows * (D / 4); w += lanes) {
+    const int lr = w / (D / 4);
+    const int d4 = (w % (D / 4)) * 4;
+    const int rho = rt * kTileRows + lr;
+    if (rho >= rows) continue;
+    float mmax = -INFINITY;
+    for (int pp = 0; pp < n_parts; pp++) mmax = fmaxf(mmax, p.partial_ml[((unit0 + pp) * kTileRows + lr) * 2]);
+    const float m_use = mmax == -INFINITY ? 0.f : mmax;
+    float4v acc = {0.f, 0.f, 0.f, 0.f};
+    float den = 0.f;
+    for (int pp = 0; pp < n_parts; pp++) {
+      const int64_t prow = (unit0 + pp) * kTileRows + lr;
+      const float wgt = exp2f(p.partial_ml[prow * 2] - m_use);
+      den += wgt * p.partial_ml[prow * 2 + 1];
+      acc += wgt * *reinterpret_cast<const float4v*>(p.partial_o + prow * D + d4);
+    }
+    const int r = rho / s.q_len, i = rho % s.q_len;
+    T* dst = static_cast<T*>(p.out) + (int64_t)(h * p.group_size + r) * p.out_stride_head +
+             (int64_t)(s.q_start + i) * p.out_stride_token + d4;
+    const float inv = 1.f / den;
+#pragma unroll
+    for (int e = 0; e < 4; e++) dst[e] = (T)(acc[e] * inv);
+  }
+}
+
 // ---------------------------------------------------------------------------
 // Split-context paged attention: one wavefront per unit.
 // ---------------------------------------------------------------------------
+// Occupancy floor (blocks per CU = wavefronts per SIMD) per dtype: the
+// largest that fits each variant without scratch.
 template <typename Tr, int D, int NB>
-__global__ __launch_bounds__(kWaveSize* kWavesPerBlock) void paged_attention_kernel(PagedAttentionParams p) {
+__global__ __launch_bounds__(kWaveSize* kWavesPerBlock, Tr::template min_blocks<NB>()) void paged_attention_kernel(
+    PagedAttentionParams p) {
   typedef typename Tr::elem T;
   constexpr int kTileRows = 16 * NB;
   __shared__ __attribute__((aligned(16))) T lds_all[kWavesPerBlock][kChunkTokens * D];
@@ -248,13 +292,17 @@ __global__ __launch_bounds__(kWaveSize* kWavesPerBlock) void paged_attention_ker
   if (unit >= p.num_units) return;
   T* lds = lds_all[wave];
 
+  // KV head fastest: the wavefronts of one (sequence, partition) read the
+  // adjacent per-head slabs of the same pages at about the same time.
   int64_t rest = unit;
+  const int h = (int)(rest % p.num_kv_heads);
+  rest /= p.num_kv_heads;
   const int part = (int)(rest % p.max_parts);
   rest /= p.max_parts;
   const int rt = (int)(rest % p.row_tiles);
-  rest /= p.row_tiles;
-  const int h = (int)(rest % p.num_kv_heads);
-  const int b = (int)(rest / p.num_kv_heads);
+  const int b = (int)(rest / p.row_tiles);
+  // Partials are stored tile-major: slot = tile * max_parts + part.
+  const int64_t slot = (((int64_t)b * p.num_kv_heads + h) * p.row_tiles + rt) * p.max_parts + part;
 
   const SeqInfo s = load_seq(p, b);
   const int rows = p.group_size * s.q_len;
@@ -377,7 +425,7 @@ __global__ __launch_bounds__(kWaveSize* kWavesPerBlock) void paged_attention_ker
         for (int n = 0; n < D / 16; n++) Tr::store_out(dst + 16 * n + 4 * g, o[nb][n] * inv);
       }
     } else {
-      const int64_t prow = unit * kTileRows + nb * 16 + (l & 15);
+      const int64_t prow = slot * kTileRows + nb * 16 + (l & 15);
       if (row_valid[nb]) {
         float* dst = p.partial_o + prow * D;
 #pragma unroll
@@ -391,8 +439,11 @@ __global__ __launch_bounds__(kWaveSize* kWavesPerBlock) void paged_attention_ker
   }
 }
 
-// Merges the context partitions of every (b, h, rt) that had more than one.
-// One 256-thread block per (b, h, rt); threads stride over (row, 4 dims).
+// Merge pass over the partitions of every tile that was split.  One
+// 256-thread block per (b, h, rt); blocks of unsplit tiles exit at once.
+// (A fused "last wavefront merges" variant with per-tile arrival counters
+// measured 43% slower on MI355X: each wavefront's device-scope release fence
+// writes back its XCD's L2, and those write-backs serialise.)
 template <typename T, int D, int NB>
 __global__ __launch_bounds__(256) void merge_partitions_kernel(PagedAttentionParams p) {
   constexpr int kTileRows = 16 * NB;
@@ -401,34 +452,10 @@ __global__ __launch_bounds__(256) void merge_partitions_kernel(PagedAttentionPar
   const int h = (tile / p.row_tiles) % p.num_kv_heads;
   const int b = tile / (p.row_tiles * p.num_kv_heads);
   const SeqInfo s = load_seq(p, b);
-  const int rows = p.group_size * s.q_len;
   const int n_chunks = tile_chunks(s, p.group_size, rt, kTileRows);
   const int n_parts = (n_chunks + p.chunks_per_part - 1) / p.chunks_per_part;
   if (n_parts <= 1) return;
-  const int64_t unit0 = (int64_t)tile * p.max_parts;
-  for (int w = threadIdx.x; w < kTileRows * (D / 4); w += blockDim.x) {
-    const int lr = w / (D / 4);
-    const int d4 = (w % (D / 4)) * 4;
-    const int rho = rt * kTileRows + lr;
-    if (rho >= rows) continue;
-    float mmax = -INFINITY;
-    for (int pp = 0; pp < n_parts; pp++) mmax = fmaxf(mmax, p.partial_ml[((unit0 + pp) * kTileRows + lr) * 2]);
-    const float m_use = mmax == -INFINITY ? 0.f : mmax;
-    float4v acc = {0.f, 0.f, 0.f, 0.f};
-    float den = 0.f;
-    for (int pp = 0; pp < n_parts; pp++) {
-      const int64_t prow = (unit0 + pp) * kTileRows + lr;
-      const float wgt = exp2f(p.partial_ml[prow * 2] - m_use);
-      den += wgt * p.partial_ml[prow * 2 + 1];
-      acc += wgt * *reinterpret_cast<const float4v*>(p.partial_o + prow * D + d4);
-    }
-    const int r = rho / s.q_len, i = rho % s.q_len;
-    T* dst = static_cast<T*>(p.out) + (int64_t)(h * p.group_size + r) * p.out_stride_head +
-             (int64_t)(s.q_start + i) * p.out_stride_token + d4;
-    const float inv = 1.f / den;
-#pragma unroll
-    for (int e = 0; e < 4; e++) dst[e] = (T)(acc[e] * inv);
-  }
+  merge_tile<T, D, NB>(p, tile, rt, h, s, n_parts, threadIdx.x, blockDim.x);
 }
 
 template <typename Tr, int D, int NB>
@@ -465,6 +492,49 @@ hipError_t launch_paged_attention(const PagedAttentionPlan& plan, PagedAttention
   }
 #undef MVR_DISPATCH
   return hipErrorInvalidValue;
+}
+
+namespace {
+
+template <typename Tr, int D, int NB>
+int64_t resident_waves_typed() {
+  // Cached per device; the query result never changes, so racing writers
+  // store the same value.
+  constexpr int kMaxDevices = 64;
+  static int64_t cache[kMaxDevices] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0) return 0;
+  if (dev < kMaxDevices && cache[dev] > 0) return cache[dev];
+  int cus = 0, blocks = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, paged_attention_kernel<Tr, D, NB>,
+                                                   kWaveSize * kWavesPerBlock, 0) != hipSuccess) {
+    (void)hipGetLastError();
+    return 0;
+  }
+  const int64_t waves = (int64_t)cus * blocks * kWavesPerBlock;
+  if (dev < kMaxDevices) cache[dev] = waves;
+  return waves;
+}
+
+} // namespace
+
+int64_t paged_attention_resident_waves(int dtype, int head_dim, int row_blocks) {
+#define MVR_OCC(TR, DD, NBV) \
+  if (head_dim == DD && row_blocks == NBV) return resident_waves_typed<TR<DD>, DD, NBV>();
+  if (dtype == 1) {
+    MVR_OCC(F16Traits, 64, 1)
+    MVR_OCC(F16Traits, 64, 2)
+    MVR_OCC(F16Traits, 128, 1)
+    MVR_OCC(F16Traits, 128, 2)
+  } else {
+    MVR_OCC(F32Traits, 64, 1)
+    MVR_OCC(F32Traits, 64, 2)
+    MVR_OCC(F32Traits, 128, 1)
+    MVR_OCC(F32Traits, 128, 2)
+  }
+#undef MVR_OCC
+  return 0;
 }
 
 } // namespace mvr

@@ -53,4 +53,8 @@ struct PagedAttentionPlan {
 
 hipError_t launch_paged_attention(const PagedAttentionPlan& plan, PagedAttentionParams params, hipStream_t stream);
 
+// Wavefronts of the plan's kernel variant the current device holds at once
+// (occupancy x waves per block x CUs); 0 if the device cannot be queried.
+int64_t paged_attention_resident_waves(int dtype, int head_dim, int row_blocks);
+
 } // namespace mvr

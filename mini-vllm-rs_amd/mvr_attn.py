@@ -211,6 +211,11 @@ def workspace_size(args: PagedAttentionArgs) -> int:
     return int(load_library().mvr_paged_attention_workspace_size(ctypes.byref(args)))
 
 
+def new_workspace(nbytes: int, device):
+    """Device scratch for context-partition partials (no initialisation needed)."""
+    return _torch().empty(max(int(nbytes), 256), dtype=_torch().uint8, device=device)
+
+
 def paged_attention(q, key_pool, value_pool, block_tables, seq_lens, cu_q_lens, out=None, *, max_q_len: int,
                     max_seq_len: int, scale: float = 0.0, workspace=None, stream=None):
     """Batched page-wise attention; returns out [Hq, total_q, D] in q's dtype."""
@@ -221,7 +226,7 @@ def paged_attention(q, key_pool, value_pool, block_tables, seq_lens, cu_q_lens, 
                   max_seq_len=max_seq_len, scale=scale, stream=stream)
     need = workspace_size(a)
     if need and (workspace is None or workspace.numel() * workspace.element_size() < need):
-        workspace = torch.empty(need, dtype=torch.uint8, device=q.device)
+        workspace = new_workspace(need, q.device)
     if workspace is not None:
         a.workspace = workspace.data_ptr()
         a.workspace_bytes = workspace.numel() * workspace.element_size()
@@ -269,7 +274,7 @@ def forward_paged_attention(request_q, layout: PagedCacheLayout, num_q_heads: in
     dt = dtype_code(q)
     lib = load_library()
     need = int(lib.mvr_forward_paged_attention_workspace_size(dt, ctypes.byref(dims), ctypes.byref(c)))
-    ws = torch.empty(max(need, 1), dtype=torch.uint8, device=q.device)
+    ws = new_workspace(need, q.device)
     _check(lib.mvr_forward_paged_attention(dt, ctypes.byref(dims), ctypes.byref(c), q.data_ptr(), y.data_ptr(),
                                            ws.data_ptr(), need, _stream_handle(stream)))
     return y

@@ -5,6 +5,7 @@ dataflow (common.rs:739-817, per-op dtype rounding); page-table indexing
 bit-exact.  Full-size workloads are also checked through size-independent
 properties (block-table relocation, poisoned unused slots, determinism).
 """
+import ctypes
 import json
 import math
 import os
@@ -194,6 +195,79 @@ def test_one_hot_gather_is_bit_exact():
             assert np.array_equal(got[h, s], want), (dtype, s, h, j)
 
 
+def test_workspace_reuse_across_shapes():
+    """One uninitialised workspace serves calls of different shapes in any order: outputs repeat bit for bit."""
+    cases = [W.qwen2_05b_batched_decode_f16(), W.llama3_8b_spec_verify_f16(), W.qwen2_05b_decode_f32(),
+             W.qwen2_7b_chunked_prefill_f16()]
+    prepared = []
+    need = 0
+    for w in cases:
+        t = W.device_tensors(w, None, seed=7)
+        out = torch.empty_like(t["q"])
+        a = M.make_args(t["q"], t["key_pool"], t["value_pool"], t["block_tables"], t["seq_lens"], t["cu_q_lens"], out,
+                        max_q_len=w.max_q_len, max_seq_len=w.max_seq_len)
+        need = max(need, M.workspace_size(a))
+        prepared.append((w, t, out, a))
+    ws = M.new_workspace(need, "cuda")
+    lib = M.load_library()
+    first = {}
+    for rnd in range(3):
+        for idx in ([0, 1, 2, 3] if rnd != 1 else [3, 1, 0, 2]):
+            w, t, out, a = prepared[idx]
+            a.workspace, a.workspace_bytes = ws.data_ptr(), ws.numel()
+            assert lib.mvr_paged_attention(ctypes.byref(a)) == 0, lib.mvr_last_error()
+            torch.cuda.synchronize()
+            if idx in first:
+                assert torch.equal(first[idx], out), (w.name, rnd)
+            else:
+                first[idx] = out.clone()
+    # fresh per-call workspaces give the same bits
+    for idx, (w, t, out, a) in enumerate(prepared):
+        again = run_hip(w, t)
+        assert torch.equal(again, first[idx])
+
+
+def test_many_small_partitions_and_many_tiles():
+    """16800 (sequence, kv head) tiles, each split into 5-7 partitions of 2 chunks (forced with
+    MVR_ATTN_CHUNKS_PER_PARTITION=2, read once per process, hence the child process): the merge of many partials
+    per tile still matches the oracle."""
+    import subprocess
+
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    path = os.pathsep.join([os.path.join(root, "mini-vllm-rs_amd"), os.path.join(root, "oracle"),
+                            os.environ.get("PYTHONPATH", "")])
+    env = dict(os.environ, MVR_ATTN_CHUNKS_PER_PARTITION="2", PYTHONPATH=path)
+    r = subprocess.run([sys.executable, "-u", __file__, "many-partitions-child"], env=env, capture_output=True,
+                       text=True, timeout=300)
+    say(r.stdout[-2000:] + r.stderr[-2000:])
+    assert r.returncode == 0
+
+
+def _many_partitions_child():
+    rng = np.random.default_rng(33)
+    B, hq, hkv, D, P = 2100, 8, 8, 64, 16
+    seq_lens = rng.integers(130, 200, size=B).astype(np.int32)
+    n = [math.ceil(int(L) / P) for L in seq_lens]
+    num_pages = sum(n)
+    perm = rng.permutation(num_pages).astype(np.int32)
+    bt = np.zeros((B, max(n)), np.int32)
+    used = 0
+    for s in range(B):
+        bt[s, :n[s]] = perm[used:used + n[s]]
+        used += n[s]
+    w = W.Workload("many tiles", "f16", hq, hkv, D, P, num_pages, 0.5, seq_lens, np.ones(B, np.int32), bt, 99)
+    vals = W.host_values(w)
+    t = W.device_tensors(w, vals)
+    a = M.make_args(t["q"], t["key_pool"], t["value_pool"], t["block_tables"], t["seq_lens"], t["cu_q_lens"],
+                    torch.empty_like(t["q"]), max_q_len=1, max_seq_len=w.max_seq_len)
+    assert M.workspace_size(a) > 0
+    out = run_hip(w, t).float().cpu().numpy()
+    ref = run_oracle(w, vals)
+    err = np.abs(out - ref).max()
+    print(f"many partitions: {B} sequences x {hkv} kv heads, max-abs vs oracle {err:.3e}", flush=True)
+    assert err <= 2e-3
+
+
 def test_full_size_properties_decode_b64():
     """Llama-3-8B batch 64 x 8K: relocating every page (and the table with it) and poisoning pages off the table
     leave the output bit-identical; two runs are bit-identical."""
@@ -228,3 +302,7 @@ def test_poisoned_tail_slots_and_foreign_pages_are_ignored():
     t2 = W.device_tensors(w, (vals[0], k, v))
     b = run_hip(w, t2)
     assert torch.equal(a, b)
+
+
+if __name__ == "__main__" and len(sys.argv) > 1 and sys.argv[1] == "many-partitions-child":
+    _many_partitions_child()
