@@ -38,7 +38,7 @@ class Runner:
         self.out = torch.empty_like(tensors["q"])
         self.args = M.make_args(tensors["q"], tensors["key_pool"], tensors["value_pool"], tensors["block_tables"],
                                 tensors["seq_lens"], tensors["cu_q_lens"], self.out, max_q_len=w.max_q_len,
-                                max_seq_len=w.max_seq_len)
+                                max_seq_len=w.max_seq_len, sum_seq_lens=int(w.seq_lens.sum()))
         need = M.workspace_size(self.args)
         self.ws = M.new_workspace(need, "cuda")
         self.args.workspace = self.ws.data_ptr()

@@ -89,6 +89,7 @@ typedef struct mvr_paged_attention_args {
   void* workspace;           /* device scratch for split-context partials */
   size_t workspace_bytes;
   void* stream;              /* hipStream_t; NULL = the null stream */
+  int64_t sum_seq_lens;      /* optional planning hint: sum of seq_lens (0 = unknown, assume max_seq_len each) */
 } mvr_paged_attention_args;
 
 /* Bytes of workspace mvr_paged_attention needs for these arguments (depends
@@ -144,6 +145,17 @@ int mvr_forward_paged_attention(int32_t dtype, const mvr_attention_dimensions* d
                                 void* workspace, size_t workspace_bytes, void* stream);
 size_t mvr_forward_paged_attention_workspace_size(int32_t dtype, const mvr_attention_dimensions* dims,
                                                   const mvr_paged_cache_layout* layout);
+
+/* reconstruct_contiguous_tensor (src/model_runner/server/kv_cache/paged_cache.rs:363-391) on the
+   device: copies the first cached_token_count tokens of the request's pages
+   (page_ids, device int32, logical order) from one pool
+   [page_count, 1, num_kv_heads, per_page_token_count, head_dim] into out
+   [1, num_kv_heads, cached_token_count, head_dim] contiguous, bit for bit.
+   Any page size.  Errors as the reference: an empty cache
+   (paged_cache.rs:383-385) and pages that do not cover the length. */
+int mvr_reconstruct_contiguous(int32_t dtype, const void* pool, int64_t page_count, int32_t num_kv_heads,
+                               int32_t per_page_token_count, int32_t head_dim, const int32_t* page_ids,
+                               int32_t num_page_ids, int32_t cached_token_count, void* out, void* stream);
 
 /* Thread-local description of the last error on this thread ("" if none). */
 const char* mvr_last_error(void);

@@ -3,6 +3,7 @@
 #include "mvr_attn.h"
 
 #include <hip/hip_runtime.h>
+#include <rocprofiler-sdk-roctx/roctx.h>
 
 #include <math.h>
 #include <stdarg.h>
@@ -10,7 +11,9 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include "kv_gather.hpp"
 #include "paged_attention_kernels.hpp"
+#include "paged_prefill.hpp"
 
 namespace {
 
@@ -33,6 +36,33 @@ int env_int(const char* name, int fallback) {
   long x = strtol(v, &end, 10);
   return (end && *end == 0 && x > 0 && x < (1L << 30)) ? (int)x : fallback;
 }
+
+// "true" / "false" as Rust's bool parser accepts them (src/utils/mod.rs:5-13);
+// anything else keeps the default instead of aborting the host process.
+bool env_bool(const char* name, bool fallback) {
+  const char* v = getenv(name);
+  if (!v) return fallback;
+  if (strcmp(v, "true") == 0) return true;
+  if (strcmp(v, "false") == 0) return false;
+  return fallback;
+}
+
+// roctx ranges named like the reference's tracing spans (trace.rs:64-116,
+// mirrored to NVTX by nvtx_trace.rs:14-53), on when MVR_ENABLE_ROCTX=true.
+bool roctx_enabled() {
+  static const bool v = env_bool("MVR_ENABLE_ROCTX", false);
+  return v;
+}
+
+struct TraceRange {
+  bool on;
+  explicit TraceRange(const char* name) : on(roctx_enabled()) {
+    if (on) roctxRangePushA(name);
+  }
+  ~TraceRange() {
+    if (on) roctxRangePop();
+  }
+};
 
 int chunks_per_partition_override() {
   static const int v = env_int("MVR_ATTN_CHUNKS_PER_PARTITION", 0);
@@ -64,6 +94,9 @@ int check_scalars(const mvr_paged_attention_args* a) {
                 mvr::kChunkTokens);
   if (a->num_pages < 1) return fail(MVR_E_INVALID_ARGUMENT, "num_pages must be positive");
   if (a->max_q_len < 1) return fail(MVR_E_INVALID_ARGUMENT, "each forward input must contain at least one token");
+  if (a->sum_seq_lens < 0 || (a->sum_seq_lens > 0 && a->sum_seq_lens > (int64_t)a->max_seq_len * a->num_seqs))
+    return fail(MVR_E_INVALID_ARGUMENT, "sum_seq_lens %lld is outside [0, num_seqs * max_seq_len]",
+                (long long)a->sum_seq_lens);
   if (a->max_seq_len < a->max_q_len)
     return fail(MVR_E_INVALID_ARGUMENT, "max_seq_len %d is smaller than max_q_len %d", a->max_seq_len, a->max_q_len);
   const int64_t pages_needed = (a->max_seq_len + a->page_size - 1) / a->page_size;
@@ -84,12 +117,46 @@ int check_scalars(const mvr_paged_attention_args* a) {
   return MVR_OK;
 }
 
+int device_cus() {
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) {
+    (void)hipGetLastError();
+    return 256; // no device to ask (sizing only): MI355X
+  }
+  return cus;
+}
+
 mvr::PagedAttentionPlan make_plan(const mvr_paged_attention_args* a) {
   mvr::PagedAttentionPlan plan{};
   plan.dtype = a->dtype;
   plan.head_dim = a->head_dim;
   const int group = a->num_q_heads / a->num_kv_heads;
   const int64_t rows_max = (int64_t)group * a->max_q_len;
+  // Many query rows per KV head (chunked prefill): dense contraction, use the
+  // LDS-shared 32x32 MFMA kernel.  MVR_ATTN_PREFILL_KERNEL=false keeps every
+  // call on the split-context kernel.
+  static const bool prefill_enabled = env_bool("MVR_ATTN_PREFILL_KERNEL", true);
+  const bool page_pow2 = (a->page_size & (a->page_size - 1)) == 0;
+  if (prefill_enabled && a->dtype == MVR_DTYPE_F16 && rows_max > 64 && page_pow2) {
+    plan.prefill = true;
+    plan.row_tiles = (int)((rows_max + mvr::kPrefillBlockRows - 1) / mvr::kPrefillBlockRows);
+    const int64_t base_blocks = (int64_t)a->num_seqs * a->num_kv_heads * plan.row_tiles;
+    const int key_tiles = (a->max_seq_len + 31) / 32;
+    static const int split_override = env_int("MVR_ATTN_PREFILL_SPLITS", 0);
+    int64_t splits = split_override;
+    if (splits <= 0) {
+      splits = 2 * (int64_t)device_cus() / base_blocks; // two 4-wavefront blocks per CU
+      if (splits > key_tiles / 8) splits = key_tiles / 8; // keep >= 8 key tiles per split
+      if (splits > 8) splits = 8;
+    }
+    if (splits < 1) splits = 1;
+    plan.kv_splits = (int)splits;
+    if (splits > 1) {
+      const size_t prow = (size_t)base_blocks * splits * mvr::kPrefillBlockRows;
+      plan.partial_bytes = align_up(prow * a->head_dim * sizeof(float), 256) + align_up(prow * 2 * sizeof(float), 256);
+    }
+    return plan;
+  }
   plan.row_blocks = rows_max <= 16 ? 1 : 2;
   const int tile_rows = 16 * plan.row_blocks;
   plan.row_tiles = (int)((rows_max + tile_rows - 1) / tile_rows);
@@ -103,10 +170,14 @@ mvr::PagedAttentionPlan make_plan(const mvr_paged_attention_args* a) {
     int64_t slots = target_waves_override();
     if (slots <= 0) slots = mvr::paged_attention_resident_waves(plan.dtype, plan.head_dim, plan.row_blocks);
     if (slots <= 0) slots = 256 * 8; // no device to ask (sizing only)
-    int64_t parts = slots / base_units;
-    if (parts < 1) parts = 1;
-    cpp = (int)((max_chunks + parts - 1) / parts);
-    if (cpp < 8) cpp = 8; // at least 128 tokens per wavefront
+    // Chunks all sequences hold, exact when the caller passes sum_seq_lens.
+    const int64_t total_chunks = a->sum_seq_lens > 0
+                                     ? (a->sum_seq_lens + mvr::kChunkTokens - 1) / mvr::kChunkTokens + a->num_seqs / 2
+                                     : (int64_t)max_chunks * a->num_seqs;
+    int64_t units_per_group = slots / ((int64_t)a->num_kv_heads * plan.row_tiles);
+    if (units_per_group < 1) units_per_group = 1;
+    const int64_t c = (total_chunks + units_per_group - 1) / units_per_group;
+    cpp = (int)(c < 8 ? 8 : (c > max_chunks ? max_chunks : c)); // at least 128 tokens per wavefront
   }
   if (cpp > max_chunks) cpp = max_chunks;
   plan.chunks_per_part = cpp;
@@ -135,6 +206,7 @@ size_t mvr_paged_attention_workspace_size(const mvr_paged_attention_args* args) 
 }
 
 int mvr_paged_attention(const mvr_paged_attention_args* a) {
+  TraceRange range("attn"); // trace.rs:64
   g_last_error[0] = 0;
   int rc = check_scalars(a);
   if (rc != MVR_OK) return rc;
@@ -144,6 +216,45 @@ int mvr_paged_attention(const mvr_paged_attention_args* a) {
                 plan.partial_bytes);
   if (plan.partial_bytes && ((uintptr_t)a->workspace & 255u))
     return fail(MVR_E_INVALID_ARGUMENT, "workspace must be 256-byte aligned");
+  const float scale = a->scale > 0.f ? a->scale : (float)(1.0 / sqrt((double)a->head_dim));
+
+  if (plan.prefill) {
+    mvr::PrefillParams f{};
+    f.q = a->q;
+    f.q_stride_head = a->q_stride_head;
+    f.q_stride_token = a->q_stride_token;
+    f.key_pool = a->key_pool;
+    f.value_pool = a->value_pool;
+    f.block_tables = a->block_tables;
+    f.block_table_stride = a->max_pages_per_seq;
+    f.seq_lens = a->seq_lens;
+    f.cu_q_lens = a->cu_q_lens;
+    f.single_seq_len = a->max_seq_len;
+    f.single_q_len = a->max_q_len;
+    f.out = a->out;
+    f.out_stride_head = a->out_stride_head;
+    f.out_stride_token = a->out_stride_token;
+    if (plan.partial_bytes) {
+      const size_t prow = (size_t)a->num_seqs * a->num_kv_heads * plan.row_tiles * plan.kv_splits *
+                          mvr::kPrefillBlockRows;
+      char* ws = static_cast<char*>(a->workspace);
+      f.partial_o = reinterpret_cast<float*>(ws);
+      f.partial_ml = reinterpret_cast<float*>(ws + align_up(prow * a->head_dim * sizeof(float), 256));
+    }
+    f.num_seqs = a->num_seqs;
+    f.num_kv_heads = a->num_kv_heads;
+    f.group_size = a->num_q_heads / a->num_kv_heads;
+    f.page_size = a->page_size;
+    f.page_shift = 0;
+    while ((1 << f.page_shift) < a->page_size) f.page_shift++; // page_size is a power of two here
+    f.row_tiles = plan.row_tiles;
+    f.kv_splits = plan.kv_splits;
+    f.scale_log2 = scale * 1.4426950408889634f;
+    TraceRange launch("attn-prefill-fused");
+    hipError_t err = mvr::launch_paged_prefill(f, a->head_dim, static_cast<hipStream_t>(a->stream));
+    if (err != hipSuccess) return fail(MVR_E_HIP, "kernel launch failed: %s", hipGetErrorString(err));
+    return MVR_OK;
+  }
 
   mvr::PagedAttentionParams p{};
   p.q = a->q;
@@ -170,9 +281,9 @@ int mvr_paged_attention(const mvr_paged_attention_args* a) {
   p.num_kv_heads = a->num_kv_heads;
   p.group_size = a->num_q_heads / a->num_kv_heads;
   p.page_size = a->page_size;
-  const float scale = a->scale > 0.f ? a->scale : (float)(1.0 / sqrt((double)a->head_dim));
   p.scale_log2 = scale * 1.4426950408889634f;
 
+  TraceRange launch("attn-paged-fused"); // one launch replaces attn-qk / attn-mask-softmax / attn-paged-v
   hipError_t err = mvr::launch_paged_attention(plan, p, static_cast<hipStream_t>(a->stream));
   if (err != hipSuccess) return fail(MVR_E_HIP, "kernel launch failed: %s", hipGetErrorString(err));
   return MVR_OK;
@@ -266,6 +377,30 @@ int mvr_forward_paged_attention(int32_t dtype, const mvr_attention_dimensions* d
   int rc = layout_to_args(dtype, dims, layout, request_q, request_y, workspace, workspace_bytes, stream, &a);
   if (rc != MVR_OK) return rc;
   return mvr_paged_attention(&a);
+}
+
+int mvr_reconstruct_contiguous(int32_t dtype, const void* pool, int64_t page_count, int32_t num_kv_heads,
+                               int32_t per_page_token_count, int32_t head_dim, const int32_t* page_ids,
+                               int32_t num_page_ids, int32_t cached_token_count, void* out, void* stream) {
+  TraceRange range("attn-cache"); // trace.rs:85, the access that materialises contiguous K/V
+  g_last_error[0] = 0;
+  if (dtype != MVR_DTYPE_F32 && dtype != MVR_DTYPE_F16)
+    return fail(MVR_E_UNSUPPORTED, "dtype %d is not F32 (0) or F16 (1)", dtype);
+  if (cached_token_count <= 0 || num_page_ids <= 0)
+    return fail(MVR_E_INVALID_ARGUMENT, "cannot reconstruct an empty KV cache"); // paged_cache.rs:383-385
+  if (num_kv_heads < 1 || per_page_token_count < 1 || head_dim < 1 || page_count < 1)
+    return fail(MVR_E_INVALID_ARGUMENT, "invalid pool geometry");
+  const int64_t covered = (int64_t)num_page_ids * per_page_token_count;
+  if (covered < cached_token_count)
+    return fail(MVR_E_PAGES_UNCOVERED,
+                "paged KV cache contains fewer pages than its sequence length, leaving %lld tokens uncovered",
+                (long long)(cached_token_count - covered));
+  if (!pool || !page_ids || !out) return fail(MVR_E_INVALID_ARGUMENT, "null pool, page ids or output pointer");
+  const int es = dtype == MVR_DTYPE_F16 ? 2 : 4;
+  hipError_t err = mvr::launch_gather_pages(pool, page_ids, num_kv_heads, per_page_token_count, head_dim, es,
+                                            cached_token_count, out, static_cast<hipStream_t>(stream));
+  if (err != hipSuccess) return fail(MVR_E_HIP, "kernel launch failed: %s", hipGetErrorString(err));
+  return MVR_OK;
 }
 
 size_t mvr_forward_paged_attention_workspace_size(int32_t dtype, const mvr_attention_dimensions* dims,

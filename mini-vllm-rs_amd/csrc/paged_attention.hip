@@ -35,6 +35,7 @@ typedef short short4v __attribute__((ext_vector_type(4)));
 typedef float float4v __attribute__((ext_vector_type(4)));
 
 typedef __attribute__((address_space(3))) short4v lds_short4;
+typedef __attribute__((address_space(4))) int32_t const_i32;
 
 __device__ __forceinline__ int lane_id() { return __lane_id(); }
 
@@ -343,7 +344,10 @@ __global__ __launch_bounds__(kWaveSize* kWavesPerBlock, Tr::template min_blocks<
 
   const T* kpool = static_cast<const T*>(p.key_pool);
   const T* vpool = static_cast<const T*>(p.value_pool);
-  const int32_t* bt = p.block_tables + (int64_t)b * p.block_table_stride;
+  // Block-table reads go through the constant address space with a uniform
+  // index, so they become scalar loads: a vector load here would make the
+  // next address wait on vmcnt(0), i.e. on every K/V load still in flight.
+  const const_i32* bt = (const const_i32*)(p.block_tables) + (int64_t)b * p.block_table_stride;
   const int chunks_per_page = p.page_size / kChunkTokens;
 
   auto slab_offset = [&](int k) -> int64_t {
@@ -389,28 +393,22 @@ __global__ __launch_bounds__(kWaveSize* kWavesPerBlock, Tr::template min_blocks<
     Tr::template pv<NB>(lds, l, pr, o);
   };
 
+  auto load_chunk = [&](int k, typename Tr::kreg_t (&kr)[Tr::kLoads], typename Tr::vreg_t (&vr)[Tr::kLoads]) {
+    const int64_t off = slab_offset(k);
+    Tr::load_k(kpool + off, l, kr);
+    Tr::load_v(vpool + off, l, vr);
+  };
+
   typename Tr::kreg_t ka[Tr::kLoads], kb[Tr::kLoads];
   typename Tr::vreg_t va[Tr::kLoads], vb[Tr::kLoads];
-  {
-    const int64_t off0 = slab_offset(k0);
-    Tr::load_k(kpool + off0, l, ka);
-    Tr::load_v(vpool + off0, l, va);
-    const int64_t off1 = slab_offset(min(k0 + 1, k1 - 1));
-    Tr::load_k(kpool + off1, l, kb);
-    Tr::load_v(vpool + off1, l, vb);
-  }
+  load_chunk(k0, ka, va);
+  load_chunk(min(k0 + 1, k1 - 1), kb, vb);
   for (int k = k0; k < k1; k += 2) {
     process(k, ka, va);
-    {
-      const int64_t off = slab_offset(min(k + 2, k1 - 1));
-      Tr::load_k(kpool + off, l, ka);
-      Tr::load_v(vpool + off, l, va);
-    }
+    load_chunk(min(k + 2, k1 - 1), ka, va);
     if (k + 1 < k1) {
       process(k + 1, kb, vb);
-      const int64_t off = slab_offset(min(k + 3, k1 - 1));
-      Tr::load_k(kpool + off, l, kb);
-      Tr::load_v(vpool + off, l, vb);
+      load_chunk(min(k + 3, k1 - 1), kb, vb);
     }
   }
 
@@ -512,7 +510,11 @@ int64_t resident_waves_typed() {
     (void)hipGetLastError();
     return 0;
   }
-  const int64_t waves = (int64_t)cus * blocks * kWavesPerBlock;
+  // Fill target: at most 2 resident wavefronts per SIMD.  Measured on the
+  // batch-64 x 8K decode, 2 per SIMD with longer partitions beat 3 per SIMD
+  // with shorter ones (371 vs 395 us): less merge traffic, fewer streams
+  // competing for the same DRAM rows.
+  const int64_t waves = (int64_t)cus * (blocks < 2 ? blocks : 2) * kWavesPerBlock;
   if (dev < kMaxDevices) cache[dev] = waves;
   return waves;
 }

@@ -49,6 +49,8 @@ struct PagedAttentionPlan {
   int max_parts;
   int64_t num_units;
   size_t partial_bytes; // workspace for partials (0 when max_parts == 1)
+  bool prefill;         // chunked-prefill kernel (paged_prefill.hip) instead of the split-context one
+  int kv_splits;        // prefill: key-range splits per 128-row tile
 };
 
 hipError_t launch_paged_attention(const PagedAttentionPlan& plan, PagedAttentionParams params, hipStream_t stream);

@@ -1,0 +1,441 @@
+// Chunked-prefill page-wise attention for gfx950 (F16, MFMA 32x32x16).
+//
+// Same contract as paged_attention.hip (common.rs:739-817 semantics: grouped
+// rows rho = r*q_len + i, key j visible to query i iff j <= seq_len - q_len + i)
+// for requests with many query rows per KV head, where attention is a dense
+// contraction (about 950 flop per byte of K/V at q_len 256) and the MFMA
+// pipes, not HBM, set the roofline.
+//
+// Block = 4 wavefronts = 128 consecutive grouped rows of one (sequence, KV
+// head); the block walks the visible keys in 32-token tiles that all four
+// wavefronts share through LDS (double-buffered, 16 KiB per stage at D=128):
+//   * K tile: 16-byte chunks, XOR swizzle (chunk ^ row%16), read back with
+//     ds_read_b128 in the v_mfma_f32_32x32x16_f16 A-operand layout
+//     (lane l: token l%32, dims 8*(l/32)+16s);  S^T = K Q^T in D/16 MFMAs;
+//   * S^T lands with lane l owning row l%32 and 16 tokens; the online softmax
+//     is exp2-based with a lazy rescale: the running max only moves (and O is
+//     only rescaled) when a score exceeds it by more than 2^8;
+//   * V tile: 32-byte-piece swizzle, ds_read_b64_tr_b16 twice per operand
+//     gives V^T in the A-operand layout; P^T (fp16) is the B operand straight
+//     from the S^T registers;  O^T += V^T P^T in D/16 MFMAs.
+// Blocks of one (sequence, KV head) are mapped onto one XCD (workgroups are
+// dispatched round-robin over the 8 XCDs), so their shared K/V stays in that
+// XCD's L2.  The key range can be split (kv_splits) to fill the device; split
+// results go to the same fp32 partial workspace as the decode kernel.
+#include "paged_prefill.hpp"
+
+#include <math.h>
+
+namespace mvr {
+namespace {
+
+typedef _Float16 half_t;
+typedef half_t half8 __attribute__((ext_vector_type(8)));
+typedef half_t half4 __attribute__((ext_vector_type(4)));
+typedef short short4v __attribute__((ext_vector_type(4)));
+typedef float float4v __attribute__((ext_vector_type(4)));
+typedef float float16v __attribute__((ext_vector_type(16)));
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) short4v lds_short4;
+typedef __attribute__((address_space(4))) int32_t const_i32;
+
+constexpr int kTileTokens = 32;
+constexpr int kRowsPerWave = 32;
+constexpr int kWaves = 4;
+constexpr int kBlockRows = kRowsPerWave * kWaves;
+constexpr int kXcds = 8;
+constexpr float kRescaleThreshold = 8.0f; // log2 units: p <= 2^8 between rescales
+
+struct SeqRows {
+  int seq_len, q_start, q_len;
+};
+
+// Block barrier that orders LDS only.  __syncthreads() also waits for every
+// outstanding global load (vmcnt(0)), which would stall on the tiles being
+// prefetched into registers; those are consumed later through ordinary
+// register dependencies, so the barrier only needs this block's LDS writes
+// to have landed.
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+__device__ __forceinline__ SeqRows load_rows(const PrefillParams& p, int b) {
+  SeqRows s;
+  s.seq_len = p.seq_lens ? p.seq_lens[b] : p.single_seq_len;
+  if (p.cu_q_lens) {
+    s.q_start = p.cu_q_lens[b];
+    s.q_len = p.cu_q_lens[b + 1] - s.q_start;
+  } else {
+    s.q_start = 0;
+    s.q_len = p.single_q_len;
+  }
+  return s;
+}
+
+// Keys the block's rows can see: up to the largest causal limit among them.
+__device__ __forceinline__ int block_key_tiles(const SeqRows& s, int group_size, int rt) {
+  const int rows = group_size * s.q_len;
+  const int rho0 = rt * kBlockRows;
+  if (rho0 >= rows || s.q_len <= 0) return 0;
+  const int rho1 = min(rho0 + kBlockRows, rows) - 1;
+  const int max_i = (rho1 / s.q_len != rho0 / s.q_len) ? s.q_len - 1 : rho1 % s.q_len;
+  const int last_key = s.seq_len - s.q_len + max_i;
+  return last_key / kTileTokens + 1;
+}
+
+template <int D>
+struct Tile {
+  static constexpr int kChunksPerRow = D / 8;                          // 16-byte chunks per token row
+  static constexpr int kChunks = kTileTokens * kChunksPerRow;          // per K (or V) tile
+  static constexpr int kChunksPerThread = kChunks / (kWaves * 64);     // 2 at D=128, 1 at D=64
+  static constexpr int kElems = kTileTokens * D;
+  // V: 32-byte pieces per row, XOR-swizzled with the row.  A transposed read
+  // is served per half-wavefront: 4 rows x 2 adjacent pieces, which must land
+  // in 8 distinct 32-byte bank groups; 2*(row&3) (D=128) spreads the 4 piece
+  // pairs apart, measured conflict-free on gfx950 (row&7 cost 2 extra
+  // cycles per read).  At D=64 two rows share a 256-byte bank line and
+  // row&3 is already conflict-free.
+  __device__ static __forceinline__ int vswz(int t) { return D == 128 ? 2 * (t & 3) : (t & 3); }
+  __device__ static __forceinline__ int kswz(int t) { return t & (kChunksPerRow - 1); }
+};
+
+template <int D>
+__global__ __launch_bounds__(kWaves * 64, 2) void paged_prefill_kernel(PrefillParams p) {
+  typedef Tile<D> TL;
+  __shared__ __attribute__((aligned(16))) half_t k_lds[3][TL::kElems];
+  __shared__ __attribute__((aligned(16))) half_t v_lds[3][TL::kElems];
+
+  const int tid = threadIdx.x;
+  const int l = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int hh = l >> 5; // lane half: 0 or 1
+
+  // XCD-aware decode of the block index: block x runs on XCD x % 8; all
+  // blocks of one (sequence, kv head) pair sit on the same XCD.
+  // With fewer pairs than XCDs, plain linear order keeps every XCD busy.
+  const int x = blockIdx.x;
+  const int per_pair = p.row_tiles * p.kv_splits;
+  const int pairs = p.num_seqs * p.num_kv_heads;
+  int pair, local;
+  if (pairs >= kXcds) {
+    const int k_on_xcd = x / kXcds;
+    pair = (x % kXcds) + kXcds * (k_on_xcd / per_pair);
+    local = k_on_xcd % per_pair;
+  } else {
+    pair = x / per_pair;
+    local = x % per_pair;
+  }
+  if (pair >= pairs) return;
+  const int h = pair % p.num_kv_heads;
+  const int b = pair / p.num_kv_heads;
+  const int split = local % p.kv_splits;
+  const int rt = local / p.kv_splits;
+
+  const SeqRows s = load_rows(p, b);
+  const int rows = p.group_size * s.q_len;
+  const int n_tiles = block_key_tiles(s, p.group_size, rt);
+  if (n_tiles == 0) return; // whole block: uniform exit before any barrier
+  const int tiles_per_split = (n_tiles + p.kv_splits - 1) / p.kv_splits;
+  const int j0 = split * tiles_per_split;
+  const int j1 = min(j0 + tiles_per_split, n_tiles);
+  const int64_t slot = (int64_t)((b * p.num_kv_heads + h) * p.row_tiles + rt) * p.kv_splits + split;
+
+  // This lane's query row.
+  const int rho = rt * kBlockRows + wave * kRowsPerWave + (l & 31);
+  const bool valid = rho < rows;
+  const int r = valid ? rho / s.q_len : 0;
+  const int i = valid ? rho % s.q_len : 0;
+  const int limit = valid ? s.seq_len - s.q_len + i : -1;
+  // Largest causal limit among the wave's rows (rows of a wave are contiguous).
+  int wave_limit = limit;
+  for (int off = 1; off < 64; off <<= 1) wave_limit = max(wave_limit, __shfl_xor(wave_limit, off));
+  int wave_min_limit = valid ? limit : INT32_MAX;
+  for (int off = 1; off < 64; off <<= 1) wave_min_limit = min(wave_min_limit, __shfl_xor(wave_min_limit, off));
+
+  // Q^T as the B operand: lane l holds Q[rho][16s + 8*hh .. +8].
+  half8 q[D / 16];
+  {
+    const half_t* qrow = static_cast<const half_t*>(p.q) + (int64_t)(h * p.group_size + r) * p.q_stride_head +
+                         (int64_t)(s.q_start + i) * p.q_stride_token;
+#pragma unroll
+    for (int st = 0; st < D / 16; st++) q[st] = valid ? *reinterpret_cast<const half8*>(qrow + 16 * st + 8 * hh) : half8{};
+  }
+
+  float16v o[D / 32];
+#pragma unroll
+  for (int n = 0; n < D / 32; n++)
+#pragma unroll
+    for (int e = 0; e < 16; e++) o[n][e] = 0.f;
+  float m = -INFINITY, lsum = 0.f;
+
+  const half_t* kpool = static_cast<const half_t*>(p.key_pool);
+  const half_t* vpool = static_cast<const half_t*>(p.value_pool);
+  // Block-table reads use the constant address space with a wave-uniform
+  // index, so they are scalar loads and never wait on the K/V loads in flight.
+  const const_i32* bt = (const const_i32*)(p.block_tables) + (int64_t)b * p.block_table_stride;
+
+  // Page arithmetic by shifts: the host routes only power-of-two page sizes
+  // (multiples of 16) to this kernel.
+  const int pshift = p.page_shift;
+  auto page_div = [&](int tok) { return tok >> pshift; };
+  auto page_mod = [&](int tok) { return tok & (p.page_size - 1); };
+
+  // Cooperative tile load: thread tid moves chunks ci = tid + 256u of K and V.
+  // The tokens one wavefront moves for a given u are 4 (D=128) or 8 (D=64)
+  // consecutive tokens inside a 16-token group, hence inside one page.
+  // Loop-invariant parts (token row, column, LDS slots) are computed once.
+  int ld_t[TL::kChunksPerThread], ld_c8[TL::kChunksPerThread], ld_t0[TL::kChunksPerThread];
+  int st_k[TL::kChunksPerThread], st_v[TL::kChunksPerThread];
+#pragma unroll
+  for (int u = 0; u < TL::kChunksPerThread; u++) {
+    const int ci = tid + kWaves * 64 * u;
+    const int t = ci / TL::kChunksPerRow, c = ci % TL::kChunksPerRow;
+    ld_t[u] = t;
+    ld_c8[u] = 8 * c;
+    ld_t0[u] = (wave * 64 + kWaves * 64 * u) / TL::kChunksPerRow;
+    st_k[u] = t * D + 8 * (c ^ TL::kswz(t));
+    st_v[u] = t * D + ((c >> 1) ^ TL::vswz(t)) * 16 + (c & 1) * 8;
+  }
+  // Branch-free: tokens past the sequence end read the last valid slot of the
+  // same page and are zeroed when stored, so the loads carry no control flow
+  // and the compiler can count outstanding loads exactly.
+  typedef u32x4 Regs[TL::kChunksPerThread];
+  auto load_tile = [&](int j, Regs& kr, Regs& vr) {
+#pragma unroll
+    for (int u = 0; u < TL::kChunksPerThread; u++) {
+      const int tg = min(j * kTileTokens + ld_t[u], s.seq_len - 1);
+      const int tg0 = min(j * kTileTokens + ld_t0[u], s.seq_len - 1);
+      const int64_t page = bt[page_div(tg0)]; // wave-uniform index: scalar load
+      const int64_t off = ((page * p.num_kv_heads + h) * p.page_size + page_mod(tg)) * D + ld_c8[u];
+      kr[u] = *reinterpret_cast<const u32x4*>(kpool + off);
+      vr[u] = *reinterpret_cast<const u32x4*>(vpool + off);
+    }
+  };
+  auto store_tile = [&](int j, const Regs& kr, const Regs& vr, int buf) {
+    half_t* kb = k_lds[buf];
+    half_t* vb = v_lds[buf];
+    if ((j + 1) * kTileTokens <= s.seq_len) { // whole tile inside the sequence (block-uniform)
+#pragma unroll
+      for (int u = 0; u < TL::kChunksPerThread; u++) {
+        *reinterpret_cast<u32x4*>(kb + st_k[u]) = kr[u];
+        *reinterpret_cast<u32x4*>(vb + st_v[u]) = vr[u];
+      }
+    } else {
+#pragma unroll
+      for (int u = 0; u < TL::kChunksPerThread; u++) {
+        const bool in_seq = j * kTileTokens + ld_t[u] < s.seq_len;
+        const u32x4 zero = {0u, 0u, 0u, 0u};
+        *reinterpret_cast<u32x4*>(kb + st_k[u]) = in_seq ? kr[u] : zero;
+        *reinterpret_cast<u32x4*>(vb + st_v[u]) = in_seq ? vr[u] : zero;
+      }
+    }
+  };
+
+  // Pipeline: 3 LDS stages and 2 register sets.  Iteration k issues the loads
+  // of tile k+2, computes tile k from stage k%3 and stores tile k+1 (loaded
+  // one iteration earlier) into stage (k+1)%3, so every load has two
+  // iterations of math to arrive.  Loads past the last tile re-read it
+  // (clamped index) and stores past it land in a stage nobody reads again:
+  // no branch around any load, so the outstanding-load count is exact.
+  Regs k0r, v0r, k1r, v1r;
+  const int j_last = max(j1 - 1, j0);
+  load_tile(j0, k0r, v0r);
+  load_tile(min(j0 + 1, j_last), k1r, v1r);
+  store_tile(j0, k0r, v0r, 0);
+  lds_barrier();
+
+  // Per-lane LDS read offsets, loop-invariant.  K: lane reads token l%32,
+  // chunk 2s+hh.  V^T: step u reads rows 16u+4hh+rsub (and +8), 16 columns
+  // at 32n+16*(g16&1)+csub, through the transposing read.
+  int rk[D / 16];
+  {
+    const int t = l & 31;
+#pragma unroll
+    for (int st = 0; st < D / 16; st++) rk[st] = t * D + 8 * ((2 * st + hh) ^ TL::kswz(t));
+  }
+  int rva[D / 32][2], rvb[D / 32][2];
+  {
+    const int g16 = l >> 4, qd = l & 15;
+    const int rsub = qd >> 2, csub = 4 * (qd & 3);
+#pragma unroll
+    for (int n = 0; n < D / 32; n++)
+#pragma unroll
+      for (int u = 0; u < 2; u++) {
+        const int row_a = 16 * u + 4 * hh + rsub, row_b = row_a + 8;
+        const int col = 32 * n + 16 * (g16 & 1) + csub;
+        rva[n][u] = row_a * D + ((col >> 4) ^ TL::vswz(row_a)) * 16 + (col & 15);
+        rvb[n][u] = row_b * D + ((col >> 4) ^ TL::vswz(row_b)) * 16 + (col & 15);
+      }
+  }
+  const float sl2 = p.scale_log2;
+
+  auto compute_tile = [&](int j, int buf) {
+    const int tok0 = j * kTileTokens;
+    // Skip the math when every row of this wave is causally past the tile.
+    if (tok0 <= wave_limit) {
+      const half_t* kb = k_lds[buf];
+      const half_t* vb = v_lds[buf];
+      float16v sc;
+#pragma unroll
+      for (int e = 0; e < 16; e++) sc[e] = 0.f;
+#pragma unroll
+      for (int st = 0; st < D / 16; st++) {
+        const half8 ka = *reinterpret_cast<const half8*>(kb + rk[st]);
+        sc = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka, q[st], sc, 0, 0, 0);
+      }
+      // Lane holds tokens tok0 + 8*(e/4) + 4*hh + e%4 of row rho (unscaled).
+      if (tok0 + kTileTokens - 1 > wave_min_limit) { // causal diagonal: mask (wave-uniform)
+#pragma unroll
+        for (int e = 0; e < 16; e++) {
+          const int tok = tok0 + 8 * (e >> 2) + 4 * hh + (e & 3);
+          sc[e] = tok <= limit ? sc[e] : -INFINITY;
+        }
+      }
+      float mx = fmaxf(fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3])), fmaxf(fmaxf(sc[4], sc[5]), fmaxf(sc[6], sc[7])));
+      mx = fmaxf(mx, fmaxf(fmaxf(fmaxf(sc[8], sc[9]), fmaxf(sc[10], sc[11])),
+                           fmaxf(fmaxf(sc[12], sc[13]), fmaxf(sc[14], sc[15]))));
+      mx *= sl2; // log2 units (scale > 0 keeps the order)
+      mx = fmaxf(mx, __shfl_xor(mx, 32));
+      const bool grow = mx > m + kRescaleThreshold || (m == -INFINITY && mx != -INFINITY);
+      if (__any(grow)) {
+        const float m_new = grow ? mx : m;
+        const float alpha = m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m - m_new);
+#pragma unroll
+        for (int n = 0; n < D / 32; n++) o[n] *= alpha;
+        lsum *= alpha;
+        m = m_new;
+      }
+      const float neg_m = m == -INFINITY ? 0.f : -m;
+      half8 pb[2];
+      float psum = 0.f;
+#pragma unroll
+      for (int e = 0; e < 16; e++) {
+        const float pe = __builtin_amdgcn_exp2f(fmaf(sc[e], sl2, neg_m)); // <= 2^8; masked: exp2(-inf) = 0
+        psum += pe;
+        pb[e >> 3][e & 7] = (half_t)pe;
+      }
+      lsum += psum;
+      // O^T += V^T P^T over two 16-token steps u; step u uses tokens
+      // 16u + 4*hh + {0..3} and 16u + 8 + 4*hh + {0..3} (the ones this lane holds).
+#pragma unroll
+      for (int n = 0; n < D / 32; n++) {
+#pragma unroll
+        for (int u = 0; u < 2; u++) {
+          const short4v ra = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4*)(vb + rva[n][u]));
+          const short4v rb = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4*)(vb + rvb[n][u]));
+          const half8 vt = __builtin_bit_cast(half8, __builtin_shufflevector(ra, rb, 0, 1, 2, 3, 4, 5, 6, 7));
+          o[n] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vt, pb[u], o[n], 0, 0, 0);
+        }
+      }
+    }
+  };
+
+  // Unrolled by two so that each register set is named statically.
+  for (int j = j0, stage = 0; j < j1; j += 2) {
+    load_tile(min(j + 2, j_last), k0r, v0r);
+    compute_tile(j, stage);
+    stage = stage == 2 ? 0 : stage + 1;
+    store_tile(j + 1, k1r, v1r, stage);
+    lds_barrier();
+    if (j + 1 >= j1) break;
+    load_tile(min(j + 3, j_last), k1r, v1r);
+    compute_tile(j + 1, stage);
+    stage = stage == 2 ? 0 : stage + 1;
+    store_tile(j + 2, k0r, v0r, stage);
+    lds_barrier();
+  }
+
+  const float ltot = lsum + __shfl_xor(lsum, 32);
+  // Lane holds O^T[d][rho] for d = 32n + 8*(e/4) + 4*hh + e%4.
+  if (p.kv_splits == 1) {
+    if (valid) {
+      const float inv = 1.f / ltot;
+      half_t* dst = static_cast<half_t*>(p.out) + (int64_t)(h * p.group_size + r) * p.out_stride_head +
+                    (int64_t)(s.q_start + i) * p.out_stride_token;
+#pragma unroll
+      for (int n = 0; n < D / 32; n++)
+#pragma unroll
+        for (int a = 0; a < 4; a++) {
+          half4 v4 = {(half_t)(o[n][4 * a] * inv), (half_t)(o[n][4 * a + 1] * inv), (half_t)(o[n][4 * a + 2] * inv),
+                      (half_t)(o[n][4 * a + 3] * inv)};
+          *reinterpret_cast<half4*>(dst + 32 * n + 8 * a + 4 * hh) = v4;
+        }
+    }
+  } else if (valid) {
+    const int64_t prow = slot * kBlockRows + wave * kRowsPerWave + (l & 31);
+    float* dst = p.partial_o + prow * D;
+#pragma unroll
+    for (int n = 0; n < D / 32; n++)
+#pragma unroll
+      for (int a = 0; a < 4; a++)
+        *reinterpret_cast<float4v*>(dst + 32 * n + 8 * a + 4 * hh) =
+            float4v{o[n][4 * a], o[n][4 * a + 1], o[n][4 * a + 2], o[n][4 * a + 3]};
+    if (hh == 0) {
+      // m is kept in log2 units of the scaled score, as the decode partials.
+      p.partial_ml[prow * 2 + 0] = m;
+      p.partial_ml[prow * 2 + 1] = ltot;
+    }
+  }
+}
+
+// Merges the kv_splits partial results of every block tile.  Empty splits
+// (no visible key) hold m = -inf, l = 0 and weigh nothing.
+template <int D>
+__global__ __launch_bounds__(256) void prefill_merge_kernel(PrefillParams p) {
+  const int tile = blockIdx.x; // (b, h, rt)
+  const int rt = tile % p.row_tiles;
+  const int h = (tile / p.row_tiles) % p.num_kv_heads;
+  const int b = tile / (p.row_tiles * p.num_kv_heads);
+  const SeqRows s = load_rows(p, b);
+  const int rows = p.group_size * s.q_len;
+  const int n_tiles = block_key_tiles(s, p.group_size, rt);
+  if (n_tiles == 0) return;
+  const int tiles_per_split = (n_tiles + p.kv_splits - 1) / p.kv_splits;
+  const int n_parts = (n_tiles + tiles_per_split - 1) / tiles_per_split; // splits that ran
+  const int64_t slot0 = (int64_t)tile * p.kv_splits;
+  for (int w = threadIdx.x; w < kBlockRows * (D / 4); w += blockDim.x) {
+    const int lr = w / (D / 4);
+    const int d4 = (w % (D / 4)) * 4;
+    const int rho = rt * kBlockRows + lr;
+    if (rho >= rows) continue;
+    float mmax = -INFINITY;
+    for (int pp = 0; pp < n_parts; pp++) mmax = fmaxf(mmax, p.partial_ml[((slot0 + pp) * kBlockRows + lr) * 2]);
+    const float m_use = mmax == -INFINITY ? 0.f : mmax;
+    float4v acc = {0.f, 0.f, 0.f, 0.f};
+    float den = 0.f;
+    for (int pp = 0; pp < n_parts; pp++) {
+      const int64_t prow = (slot0 + pp) * kBlockRows + lr;
+      const float mp = p.partial_ml[prow * 2];
+      const float wgt = mp == -INFINITY ? 0.f : exp2f(mp - m_use);
+      den += wgt * p.partial_ml[prow * 2 + 1];
+      acc += wgt * *reinterpret_cast<const float4v*>(p.partial_o + prow * D + d4);
+    }
+    const int r = rho / s.q_len, i = rho % s.q_len;
+    half_t* dst = static_cast<half_t*>(p.out) + (int64_t)(h * p.group_size + r) * p.out_stride_head +
+                  (int64_t)(s.q_start + i) * p.out_stride_token + d4;
+    const float inv = 1.f / den;
+#pragma unroll
+    for (int e = 0; e < 4; e++) dst[e] = (half_t)(acc[e] * inv);
+  }
+}
+
+template <int D>
+hipError_t launch_typed(const PrefillParams& params, hipStream_t stream) {
+  const int pairs = params.num_seqs * params.num_kv_heads;
+  const int per_pair = params.row_tiles * params.kv_splits;
+  const int64_t blocks =
+      pairs >= kXcds ? (int64_t)kXcds * ((pairs + kXcds - 1) / kXcds) * per_pair : (int64_t)pairs * per_pair;
+  hipLaunchKernelGGL(paged_prefill_kernel<D>, dim3((unsigned)blocks), dim3(kWaves * 64), 0, stream, params);
+  hipError_t err = hipGetLastError();
+  if (err != hipSuccess || params.kv_splits == 1) return err;
+  hipLaunchKernelGGL(prefill_merge_kernel<D>, dim3(pairs * params.row_tiles), dim3(256), 0, stream, params);
+  return hipGetLastError();
+}
+
+} // namespace
+
+hipError_t launch_paged_prefill(const PrefillParams& params, int head_dim, hipStream_t stream) {
+  if (head_dim == 128) return launch_typed<128>(params, stream);
+  if (head_dim == 64) return launch_typed<64>(params, stream);
+  return hipErrorInvalidValue;
+}
+
+} // namespace mvr

@@ -1,0 +1,35 @@
+// Internal launch interface of the chunked-prefill kernel (paged_prefill.hip).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace mvr {
+
+// Rows per block of the prefill kernel (4 wavefronts x 32 grouped rows).
+constexpr int kPrefillBlockRows = 128;
+
+struct PrefillParams {
+  const void* q;
+  int64_t q_stride_head, q_stride_token;
+  const void* key_pool;
+  const void* value_pool;
+  const int32_t* block_tables;
+  int32_t block_table_stride;
+  const int32_t* seq_lens;  // may be null: single_seq_len
+  const int32_t* cu_q_lens; // may be null: single_q_len
+  int32_t single_seq_len, single_q_len;
+  void* out;
+  int64_t out_stride_head, out_stride_token;
+  float* partial_o;  // [slots][128][head_dim] fp32 when kv_splits > 1
+  float* partial_ml; // [slots][128][2]
+  int32_t num_seqs, num_kv_heads, group_size, page_size;
+  int32_t page_shift; // log2(page_size); page_size is a power of two
+  int32_t row_tiles;  // 128-row tiles per (sequence, kv head)
+  int32_t kv_splits; // key-range splits per row tile
+  float scale_log2;
+};
+
+hipError_t launch_paged_prefill(const PrefillParams& params, int head_dim, hipStream_t stream);
+
+} // namespace mvr

@@ -42,6 +42,7 @@ EXPORTED_SYMBOLS = (
     "mvr_paged_attention_validate",
     "mvr_forward_paged_attention",
     "mvr_forward_paged_attention_workspace_size",
+    "mvr_reconstruct_contiguous",
 )
 
 
@@ -79,6 +80,7 @@ class PagedAttentionArgs(ctypes.Structure):
         ("workspace", ctypes.c_void_p),
         ("workspace_bytes", ctypes.c_size_t),
         ("stream", ctypes.c_void_p),
+        ("sum_seq_lens", ctypes.c_int64),
     ]
 
 
@@ -135,6 +137,10 @@ def load_library():
     lib.mvr_forward_paged_attention_workspace_size.restype = ctypes.c_size_t
     lib.mvr_forward_paged_attention_workspace_size.argtypes = [ctypes.c_int32, ctypes.POINTER(AttentionDimensions),
                                                                ctypes.POINTER(PagedCacheLayoutC)]
+    lib.mvr_reconstruct_contiguous.restype = ctypes.c_int
+    lib.mvr_reconstruct_contiguous.argtypes = [ctypes.c_int32, ctypes.c_void_p, ctypes.c_int64, ctypes.c_int32,
+                                               ctypes.c_int32, ctypes.c_int32, ctypes.c_void_p, ctypes.c_int32,
+                                               ctypes.c_int32, ctypes.c_void_p, ctypes.c_void_p]
     if lib.mvr_abi_version() != 1:
         raise RuntimeError("libmvr_attn.so ABI version mismatch")
     _lib = lib
@@ -170,7 +176,7 @@ def _stream_handle(stream) -> Optional[int]:
 
 
 def make_args(q, key_pool, value_pool, block_tables, seq_lens, cu_q_lens, out, *, max_q_len: int,
-              max_seq_len: int, scale: float = 0.0, stream=None) -> PagedAttentionArgs:
+              max_seq_len: int, scale: float = 0.0, stream=None, sum_seq_lens: int = 0) -> PagedAttentionArgs:
     """Fills the C argument struct.  q / out: [Hq, total_q, D] (last dim contiguous);
     pools: [num_pages, 1, Hkv, page_size, D]; block_tables int32 [num_seqs, max_pages]."""
     n_pages, one, hkv, page_size, d = key_pool.shape
@@ -204,6 +210,7 @@ def make_args(q, key_pool, value_pool, block_tables, seq_lens, cu_q_lens, out, *
     a.out_stride_head = out.stride(0)
     a.out_stride_token = out.stride(1)
     a.stream = _stream_handle(stream)
+    a.sum_seq_lens = int(sum_seq_lens)
     return a
 
 
@@ -217,13 +224,13 @@ def new_workspace(nbytes: int, device):
 
 
 def paged_attention(q, key_pool, value_pool, block_tables, seq_lens, cu_q_lens, out=None, *, max_q_len: int,
-                    max_seq_len: int, scale: float = 0.0, workspace=None, stream=None):
+                    max_seq_len: int, scale: float = 0.0, workspace=None, stream=None, sum_seq_lens: int = 0):
     """Batched page-wise attention; returns out [Hq, total_q, D] in q's dtype."""
     torch = _torch()
     if out is None:
         out = torch.empty_like(q, memory_format=torch.contiguous_format)
     a = make_args(q, key_pool, value_pool, block_tables, seq_lens, cu_q_lens, out, max_q_len=max_q_len,
-                  max_seq_len=max_seq_len, scale=scale, stream=stream)
+                  max_seq_len=max_seq_len, scale=scale, stream=stream, sum_seq_lens=sum_seq_lens)
     need = workspace_size(a)
     if need and (workspace is None or workspace.numel() * workspace.element_size() < need):
         workspace = new_workspace(need, q.device)
@@ -278,6 +285,19 @@ def forward_paged_attention(request_q, layout: PagedCacheLayout, num_q_heads: in
     _check(lib.mvr_forward_paged_attention(dt, ctypes.byref(dims), ctypes.byref(c), q.data_ptr(), y.data_ptr(),
                                            ws.data_ptr(), need, _stream_handle(stream)))
     return y
+
+
+def reconstruct_contiguous(pool, page_ids, cached_token_count: int, stream=None):
+    """reconstruct_contiguous_tensor (paged_cache.rs:363-391): pool [N, 1, Hkv, P, D], page_ids int32 (device)
+    -> [1, Hkv, cached_token_count, D], bit-exact."""
+    torch = _torch()
+    n, _, hkv, page_size, d = pool.shape
+    out = torch.empty((1, hkv, max(int(cached_token_count), 0), d), dtype=pool.dtype, device=pool.device)
+    rc = load_library().mvr_reconstruct_contiguous(dtype_code(pool), pool.data_ptr(), n, hkv, page_size, d,
+                                                   page_ids.data_ptr(), page_ids.numel(), int(cached_token_count),
+                                                   out.data_ptr(), _stream_handle(stream))
+    _check(rc)
+    return out
 
 
 def pages_for(seq_len: int, page_size: int) -> int:

@@ -128,6 +128,17 @@ def test_request_level_entry_checks_lengths():
     assert "leaving 16 tokens uncovered" in lib.mvr_last_error().decode()
 
 
+def test_reconstruct_contiguous_rejects_like_the_reference():
+    lib = M.load_library()
+    rc = lib.mvr_reconstruct_contiguous(M.DTYPE_F16, 1 << 20, 8, 2, 16, 64, 1 << 20, 0, 0, 1 << 20, None)
+    assert rc == M.MVR_E_INVALID_ARGUMENT
+    assert "cannot reconstruct an empty KV cache" in lib.mvr_last_error().decode()  # paged_cache.rs:383-385
+    rc = lib.mvr_reconstruct_contiguous(M.DTYPE_F16, 1 << 20, 8, 2, 16, 64, 1 << 20, 2, 40, 1 << 20, None)
+    assert rc == M.MVR_E_PAGES_UNCOVERED and "leaving 8 tokens uncovered" in lib.mvr_last_error().decode()
+    rc = lib.mvr_reconstruct_contiguous(5, 1 << 20, 8, 2, 16, 64, 1 << 20, 2, 20, 1 << 20, None)
+    assert rc == M.MVR_E_UNSUPPORTED
+
+
 def test_workloads_match_stated_sizes():
     import workloads as W
 
