@@ -241,40 +241,6 @@ struct F32Traits {
   __device__ static __forceinline__ void store_out(float* dst, float4v v) { *reinterpret_cast<float4v*>(dst) = v; }
 };
 
-// Merges the n_parts partial results of tile (b, h, rt) and writes the
-// normalised output: out = sum_p 2^(m_p - M) o_p / sum_p 2^(m_p - M) l_p.
-// Executed by `lanes` threads with ids lane0 .. lane0+lanes-1.
-template <typename T, int D, int NB>
-__device__ __forceinline__ void merge_tile(const PagedAttentionParams& p, int64_t tile, int rt, int h, const SeqInfo& s,
-                                           int n_parts, int lane0, int lanes) {
-  constexpr int kTileRows = 16 * NB;
-  const int rows = p.group_size * s.q_len;
-  const int64_t unit0 = tile * p.max_parts;
-  for (int w = lane0; w < kTileRows * (D / 4); w += lanes) {
-    const int lr = w / (D / 4);
-    const int d4 = (w % (D / 4)) * 4;
-    const int rho = rt * kTileRows + lr;
-    if (rho >= rows) continue;
-    float mmax = -INFINITY;
-    for (int pp = 0; pp < n_parts; pp++) mmax = fmaxf(mmax, p.partial_ml[((unit0 + pp) * kTileRows + lr) * 2]);
-    const float m_use = mmax == -INFINITY ? 0.f : mmax;
-    float4v acc = {0.f, 0.f, 0.f, 0.f};
-    float den = 0.f;
-    for (int pp = 0; pp < n_parts; pp++) {
-      const int64_t prow = (unit0 + pp) * kTileRows + lr;
-      const float wgt = exp2f(p.partial_ml[prow * 2] - m_use);
-      den += wgt * p.partial_ml[prow * 2 + 1];
-      acc += wgt * *reinterpret_cast<const float4v*>(p.partial_o + prow * D + d4);
-    }
-    const int r = rho / s.q_len, i = rho % s.q_len;
-    T* dst = static_cast<T*>(p.out) + (int64_t)(h * p.group_size + r) * p.out_stride_head +
-             (int64_t)(s.q_start + i) * p.out_stride_token + d4;
-    const float inv = 1.f / den;
-#pragma unroll
-    for (int e = 0; e < 4; e++) dst[e] = (T)(acc[e] * inv);
-  }
-}
-
 // ---------------------------------------------------------------------------
 // Split-context paged attention: one wavefront per unit.
 // ---------------------------------------------------------------------------
@@ -294,7 +260,11 @@ __global__ __launch_bounds__(kWaveSize* kWavesPerBlock, Tr::template min_blocks<
   T* lds = lds_all[wave];
 
   // KV head fastest: the wavefronts of one (sequence, partition) read the
-  // adjacent per-head slabs of the same pages at about the same time.
+  // adjacent per-head slabs of the same pages at about the same time.  The
+  // planner pads max_parts so that a sequence spans a multiple of 8 blocks:
+  // the dispatcher deals blocks to the 8 XCDs round-robin, so partition
+  // `part` of KV head h runs on the same XCD for every sequence, and pages
+  // shared by several sequences (a common prefix) hit in that XCD's L2.
   int64_t rest = unit;
   const int h = (int)(rest % p.num_kv_heads);
   rest /= p.num_kv_heads;
@@ -437,23 +407,84 @@ __global__ __launch_bounds__(kWaveSize* kWavesPerBlock, Tr::template min_blocks<
   }
 }
 
-// Merge pass over the partitions of every tile that was split.  One
-// 256-thread block per (b, h, rt); blocks of unsplit tiles exit at once.
+// Merge pass over the partitions of every tile that was split:
+//   out = sum_j 2^(m_j - M) o_j / sum_j 2^(m_j - M) l_j,  M = max_j m_j.
+// One wavefront per (b, h, rt, row); a 256-thread block covers 4 rows of one
+// tile.  Lane j holds partition j's weight (64 partitions per round), the
+// partial rows are streamed as one coalesced 4*D-byte row per load with the
+// weight broadcast by readlane, eight rows in flight.  Rows and tiles that
+// were not split exit at once.
 // (A fused "last wavefront merges" variant with per-tile arrival counters
 // measured 43% slower on MI355X: each wavefront's device-scope release fence
 // writes back its XCD's L2, and those write-backs serialise.)
 template <typename T, int D, int NB>
 __global__ __launch_bounds__(256) void merge_partitions_kernel(PagedAttentionParams p) {
   constexpr int kTileRows = 16 * NB;
-  const int tile = blockIdx.x;
+  constexpr int kBlocksPerTile = kTileRows / kWavesPerBlock;
+  constexpr int kPer = D / kWaveSize; // output elements per lane
+  constexpr int kInFlight = 8;
+  const int tile = blockIdx.x / kBlocksPerTile;
+  const int lr = (blockIdx.x % kBlocksPerTile) * kWavesPerBlock + __builtin_amdgcn_readfirstlane(threadIdx.x / kWaveSize);
+  const int l = lane_id();
   const int rt = tile % p.row_tiles;
   const int h = (tile / p.row_tiles) % p.num_kv_heads;
   const int b = tile / (p.row_tiles * p.num_kv_heads);
   const SeqInfo s = load_seq(p, b);
+  const int rho = rt * kTileRows + lr;
+  if (rho >= p.group_size * s.q_len) return;
   const int n_chunks = tile_chunks(s, p.group_size, rt, kTileRows);
   const int n_parts = (n_chunks + p.chunks_per_part - 1) / p.chunks_per_part;
   if (n_parts <= 1) return;
-  merge_tile<T, D, NB>(p, tile, rt, h, s, n_parts, threadIdx.x, blockDim.x);
+
+  // Partial row of partition j: (tile * max_parts + j) * kTileRows + lr.
+  const int64_t prow0 = (int64_t)tile * p.max_parts * kTileRows + lr;
+  float mmax = -INFINITY;
+  for (int j = l; j < n_parts; j += kWaveSize) mmax = fmaxf(mmax, p.partial_ml[(prow0 + (int64_t)j * kTileRows) * 2]);
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) mmax = fmaxf(mmax, __shfl_xor(mmax, off));
+  const float m_use = mmax == -INFINITY ? 0.f : mmax;
+
+  float den = 0.f;
+  float acc[kPer];
+#pragma unroll
+  for (int e = 0; e < kPer; e++) acc[e] = 0.f;
+  for (int j0 = 0; j0 < n_parts; j0 += kWaveSize) {
+    float w = 0.f;
+    if (j0 + l < n_parts) {
+      const int64_t prow = prow0 + (int64_t)(j0 + l) * kTileRows;
+      w = __builtin_amdgcn_exp2f(p.partial_ml[prow * 2] - m_use); // m = -inf (no visible key) gives 0
+      den += w * p.partial_ml[prow * 2 + 1];
+    }
+    const int cnt = min(kWaveSize, n_parts - j0);
+    const float* base = p.partial_o + (prow0 + (int64_t)j0 * kTileRows) * D + l * kPer;
+    int jj = 0;
+    for (; jj + kInFlight <= cnt; jj += kInFlight) {
+      float v[kInFlight][kPer];
+#pragma unroll
+      for (int u = 0; u < kInFlight; u++)
+#pragma unroll
+        for (int e = 0; e < kPer; e++) v[u][e] = base[(int64_t)(jj + u) * kTileRows * D + e];
+#pragma unroll
+      for (int u = 0; u < kInFlight; u++) {
+        const float wu = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), jj + u));
+#pragma unroll
+        for (int e = 0; e < kPer; e++) acc[e] = fmaf(wu, v[u][e], acc[e]);
+      }
+    }
+    for (; jj < cnt; jj++) {
+      const float wu = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), jj));
+#pragma unroll
+      for (int e = 0; e < kPer; e++) acc[e] = fmaf(wu, base[(int64_t)jj * kTileRows * D + e], acc[e]);
+    }
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) den += __shfl_xor(den, off);
+  const int r = rho / s.q_len, i = rho % s.q_len;
+  T* dst = static_cast<T*>(p.out) + (int64_t)(h * p.group_size + r) * p.out_stride_head +
+           (int64_t)(s.q_start + i) * p.out_stride_token + l * kPer;
+  const float inv = 1.f / den;
+#pragma unroll
+  for (int e = 0; e < kPer; e++) dst[e] = (T)(acc[e] * inv);
 }
 
 template <typename Tr, int D, int NB>
@@ -463,8 +494,9 @@ hipError_t launch_typed(const PagedAttentionPlan& plan, const PagedAttentionPara
                      stream, params);
   hipError_t err = hipGetLastError();
   if (err != hipSuccess || plan.max_parts <= 1) return err;
-  const int tiles = params.num_seqs * params.num_kv_heads * params.row_tiles;
-  hipLaunchKernelGGL((merge_partitions_kernel<typename Tr::elem, D, NB>), dim3(tiles), dim3(256), 0, stream, params);
+  const int64_t tiles = (int64_t)params.num_seqs * params.num_kv_heads * params.row_tiles;
+  hipLaunchKernelGGL((merge_partitions_kernel<typename Tr::elem, D, NB>), dim3((unsigned)(tiles * 4 * NB)),
+                     dim3(kWaveSize * kWavesPerBlock), 0, stream, params);
   return hipGetLastError();
 }
 
