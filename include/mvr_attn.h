@@ -60,7 +60,9 @@ typedef enum {
   /* a page id outside [0, num_pages) (Tensor::narrow fails in the reference) */
   MVR_E_PAGE_ID = -5,
   MVR_E_WORKSPACE = -6,
-  MVR_E_HIP = -7
+  MVR_E_HIP = -7,
+  /* physical_page_pool.rs:197-201: "cannot mutate written physical page N" */
+  MVR_E_READ_ONLY_PAGE = -8
 } mvr_status;
 
 typedef struct mvr_paged_attention_args {
@@ -156,6 +158,70 @@ size_t mvr_forward_paged_attention_workspace_size(int32_t dtype, const mvr_atten
 int mvr_reconstruct_contiguous(int32_t dtype, const void* pool, int64_t page_count, int32_t num_kv_heads,
                                int32_t per_page_token_count, int32_t head_dim, const int32_t* page_ids,
                                int32_t num_page_ids, int32_t cached_token_count, void* out, void* stream);
+
+/* RotaryEmbeddingType (common.rs:552-556): Neox rotates dims (i, i + D/2)
+   (candle-nn rope), Interleaved rotates (2i, 2i + 1) (candle-nn rope_i). */
+typedef enum { MVR_ROPE_NEOX = 0, MVR_ROPE_INTERLEAVED = 1 } mvr_rope_type;
+
+/* The step before attention for every request of a layer: rotary embedding
+   of the new Q and K rows and the append of K/V into their page slots.
+   Uses the same block tables, seq_lens and cu_q_lens as the attention call
+   that follows it: seq_lens counts the tokens after this append, so request
+   b's new tokens sit at positions seq_lens[b] - q_len .. seq_lens[b] - 1.
+   The block table rows must already hold the pages those positions fall in
+   (the host allocates pages; this call only writes). */
+typedef struct mvr_rope_append_args {
+  int32_t dtype;             /* mvr_dtype */
+  int32_t rope_type;         /* mvr_rope_type */
+  int32_t num_seqs;
+  int32_t num_q_heads;
+  int32_t num_kv_heads;      /* divides num_q_heads */
+  int32_t head_dim;          /* a multiple of 8, at most 512 */
+  int32_t page_size;         /* per_page_token_count, any positive value */
+  int64_t num_pages;
+  int32_t max_pages_per_seq; /* row stride of block_tables */
+  int32_t total_q;           /* packed new tokens = cu_q_lens[num_seqs] (sizes the grid) */
+  int32_t max_seq_len;       /* >= every seq_len */
+  int32_t rope_len;          /* rows of the cos / sin tables; >= max_seq_len */
+  const void* q;             /* [Hq, total_q, D] through strides (elements) */
+  int64_t q_stride_head, q_stride_token;
+  const void* k;             /* [Hkv, total_q, D] */
+  int64_t k_stride_head, k_stride_token;
+  const void* v;             /* [Hkv, total_q, D] */
+  int64_t v_stride_head, v_stride_token;
+  const void* cos_table;     /* [rope_len, D/2] contiguous, activation dtype (RotaryEmbeddingContext::cos) */
+  const void* sin_table;     /* [rope_len, D/2] */
+  const int32_t* block_tables; /* device */
+  const int32_t* seq_lens;     /* device; NULL allowed when num_seqs == 1: seq_len = max_seq_len */
+  const int32_t* cu_q_lens;    /* device; NULL allowed when num_seqs == 1: q_len = total_q */
+  void* q_out;               /* rotated queries; may be q itself (in place) */
+  int64_t q_out_stride_head, q_out_stride_token;
+  void* key_pool;            /* written: rotated keys */
+  void* value_pool;          /* written: values */
+  void* stream;              /* hipStream_t */
+} mvr_rope_append_args;
+
+/* forward_rope for Q and K (common.rs:294-307, :344-359) and
+   append_new_key_value (kv_cache/paged_cache.rs:170-199, :290-327;
+   physical_page_pool.rs:188-209) fused into one launch over every request
+   (replaces the per-request part of forward_attention's loop,
+   common.rs:285-320).  Arithmetic in the activation dtype with each product
+   and sum rounded as the reference's rope kernels do.  Stream-ordered;
+   allocates nothing; device tables are trusted (see
+   mvr_rope_append_validate). */
+int mvr_rope_append(const mvr_rope_append_args* args);
+
+/* Host-side checks of the tables the append will use, mirroring the
+   reference's errors: every q_len >= 1 ("cannot append an empty KV-cache
+   tensor", kv_cache/utils.rs:33-36), seq_len >= q_len, pages covering every
+   position written, page ids inside the pool, no page written by two
+   requests, positions inside the rotary tables, and, when page_writable_host
+   (one byte per pool page, nonzero = PendingWrite) is given, that every page
+   written is writable ("cannot mutate written physical page N",
+   physical_page_pool.rs:197-201).  Launches nothing. */
+int mvr_rope_append_validate(const mvr_rope_append_args* args, const int32_t* block_tables_host,
+                             const int32_t* seq_lens_host, const int32_t* cu_q_lens_host,
+                             const uint8_t* page_writable_host);
 
 /* Thread-local description of the last error on this thread ("" if none). */
 const char* mvr_last_error(void);

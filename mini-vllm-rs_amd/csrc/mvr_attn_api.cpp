@@ -11,6 +11,7 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include "kv_append.hpp"
 #include "kv_gather.hpp"
 #include "paged_attention_kernels.hpp"
 #include "paged_prefill.hpp"
@@ -230,6 +231,150 @@ extern "C" {
 int mvr_abi_version(void) { return MVR_ATTN_ABI_VERSION; }
 
 const char* mvr_last_error(void) { return g_last_error; }
+
+// ---------------------------------------------------------------------------
+// RoPE + KV append
+// ---------------------------------------------------------------------------
+
+static int check_rope_append(const mvr_rope_append_args* a) {
+  if (!a) return fail(MVR_E_INVALID_ARGUMENT, "args is null");
+  if (a->dtype != MVR_DTYPE_F32 && a->dtype != MVR_DTYPE_F16)
+    return fail(MVR_E_UNSUPPORTED, "dtype %d is not F32 (0) or F16 (1)", a->dtype);
+  if (a->rope_type != MVR_ROPE_NEOX && a->rope_type != MVR_ROPE_INTERLEAVED)
+    return fail(MVR_E_UNSUPPORTED, "rope_type %d is not Neox (0) or Interleaved (1)", a->rope_type);
+  if (a->num_seqs < 1) return fail(MVR_E_INVALID_ARGUMENT, "forward requires at least one request");
+  if (a->num_kv_heads < 1 || a->num_q_heads < 1 || a->num_q_heads % a->num_kv_heads != 0)
+    return fail(MVR_E_INVALID_ARGUMENT, "num_q_heads %d is not a multiple of num_kv_heads %d", a->num_q_heads,
+                a->num_kv_heads);
+  if (a->head_dim < 8 || a->head_dim > 512 || a->head_dim % 8 != 0)
+    return fail(MVR_E_UNSUPPORTED, "head_dim %d is not a multiple of 8 in [8, 512]", a->head_dim);
+  if (a->page_size < 1) return fail(MVR_E_INVALID_ARGUMENT, "page_size must be positive");
+  if (a->num_pages < 1) return fail(MVR_E_INVALID_ARGUMENT, "num_pages must be positive");
+  if (a->total_q < 1) return fail(MVR_E_INVALID_ARGUMENT, "cannot append an empty KV-cache tensor"); // kv_cache/utils.rs:33-36
+  if (a->num_seqs > a->total_q) return fail(MVR_E_INVALID_ARGUMENT, "cannot append an empty KV-cache tensor");
+  if (a->max_seq_len < 1) return fail(MVR_E_INVALID_ARGUMENT, "max_seq_len must be positive");
+  if (a->rope_len < a->max_seq_len)
+    return fail(MVR_E_INVALID_ARGUMENT, "rotary tables hold %d positions, max_seq_len is %d", a->rope_len,
+                a->max_seq_len);
+  const int64_t pages_needed = (a->max_seq_len + (int64_t)a->page_size - 1) / a->page_size;
+  if (a->max_pages_per_seq < pages_needed)
+    return fail(MVR_E_PAGES_UNCOVERED, "block table rows of %d pages cannot hold %d tokens of %d-token pages",
+                a->max_pages_per_seq, a->max_seq_len, a->page_size);
+  if (a->num_seqs > 1 && (!a->seq_lens || !a->cu_q_lens))
+    return fail(MVR_E_INVALID_ARGUMENT, "seq_lens and cu_q_lens are required when num_seqs > 1");
+  if (!a->q || !a->k || !a->v || !a->cos_table || !a->sin_table || !a->block_tables || !a->q_out || !a->key_pool ||
+      !a->value_pool)
+    return fail(MVR_E_INVALID_ARGUMENT, "null tensor, table or pool pointer");
+  const int64_t vec = 4; // every access moves 4 elements: 8 bytes (F16) or 16 bytes (F32)
+  const size_t align = a->dtype == MVR_DTYPE_F16 ? 8 : 16;
+  const void* ptrs[] = {a->q, a->k, a->v, a->cos_table, a->sin_table, a->q_out, a->key_pool, a->value_pool};
+  for (const void* ptr : ptrs)
+    if ((uintptr_t)ptr % align)
+      return fail(MVR_E_INVALID_ARGUMENT, "tensors, tables and pools must be %zu-byte aligned", align);
+  const int64_t strides[] = {a->q_stride_head, a->q_stride_token, a->k_stride_head,     a->k_stride_token,
+                             a->v_stride_head, a->v_stride_token, a->q_out_stride_head, a->q_out_stride_token};
+  for (int64_t st : strides)
+    if (st % vec) return fail(MVR_E_INVALID_ARGUMENT, "strides must be multiples of %lld elements", (long long)vec);
+  return MVR_OK;
+}
+
+int mvr_rope_append(const mvr_rope_append_args* a) {
+  TraceRange range("attn-cache"); // trace.rs: attention_cache_append
+  g_last_error[0] = 0;
+  int rc = check_rope_append(a);
+  if (rc != MVR_OK) return rc;
+  mvr::RopeAppendParams p{};
+  p.q = a->q;
+  p.q_stride_head = a->q_stride_head;
+  p.q_stride_token = a->q_stride_token;
+  p.k = a->k;
+  p.k_stride_head = a->k_stride_head;
+  p.k_stride_token = a->k_stride_token;
+  p.v = a->v;
+  p.v_stride_head = a->v_stride_head;
+  p.v_stride_token = a->v_stride_token;
+  p.cos_table = a->cos_table;
+  p.sin_table = a->sin_table;
+  p.block_tables = a->block_tables;
+  p.block_table_stride = a->max_pages_per_seq;
+  p.seq_lens = a->seq_lens;
+  p.cu_q_lens = a->cu_q_lens;
+  p.single_seq_len = a->max_seq_len;
+  p.q_out = a->q_out;
+  p.q_out_stride_head = a->q_out_stride_head;
+  p.q_out_stride_token = a->q_out_stride_token;
+  p.key_pool = a->key_pool;
+  p.value_pool = a->value_pool;
+  p.num_seqs = a->num_seqs;
+  p.num_q_heads = a->num_q_heads;
+  p.num_kv_heads = a->num_kv_heads;
+  p.head_dim = a->head_dim;
+  p.page_size = a->page_size;
+  p.total_q = a->total_q;
+  hipError_t err = mvr::launch_rope_append(p, a->dtype, a->rope_type, static_cast<hipStream_t>(a->stream));
+  if (err != hipSuccess) return fail(MVR_E_HIP, "kernel launch failed: %s", hipGetErrorString(err));
+  return MVR_OK;
+}
+
+int mvr_rope_append_validate(const mvr_rope_append_args* a, const int32_t* block_tables_host,
+                             const int32_t* seq_lens_host, const int32_t* cu_q_lens_host,
+                             const uint8_t* page_writable_host) {
+  g_last_error[0] = 0;
+  int rc = check_rope_append(a);
+  if (rc != MVR_OK) return rc;
+  if (cu_q_lens_host) {
+    if (cu_q_lens_host[0] != 0) return fail(MVR_E_INVALID_ARGUMENT, "cu_q_lens[0] must be 0");
+    if (cu_q_lens_host[a->num_seqs] != a->total_q)
+      return fail(MVR_E_INVALID_ARGUMENT, "cu_q_lens[num_seqs] = %d, total_q = %d", cu_q_lens_host[a->num_seqs],
+                  a->total_q);
+  }
+  // Pages written by an earlier request of this call (a page is PendingWrite
+  // for one request only; two writers would race).
+  uint8_t* owner_seen = nullptr;
+  if (block_tables_host) {
+    owner_seen = static_cast<uint8_t*>(calloc((size_t)a->num_pages, 1));
+    if (!owner_seen) return fail(MVR_E_INVALID_ARGUMENT, "out of host memory");
+  }
+  rc = MVR_OK;
+  for (int s = 0; s < a->num_seqs && rc == MVR_OK; s++) {
+    const int q_len = cu_q_lens_host ? cu_q_lens_host[s + 1] - cu_q_lens_host[s] : (a->num_seqs == 1 ? a->total_q : -1);
+    const int seq_len = seq_lens_host ? seq_lens_host[s] : (a->num_seqs == 1 ? a->max_seq_len : -1);
+    if (q_len == 0 || (q_len < 0 && cu_q_lens_host)) {
+      rc = fail(MVR_E_INVALID_ARGUMENT, "cannot append an empty KV-cache tensor"); // kv_cache/utils.rs:33-36
+      break;
+    }
+    if (seq_len < 0 || q_len < 0) continue;
+    if (seq_len > a->max_seq_len) {
+      rc = fail(MVR_E_INVALID_ARGUMENT, "request %d has seq_len %d > max_seq_len %d", s, seq_len, a->max_seq_len);
+      break;
+    }
+    if (seq_len < q_len) {
+      rc = fail(MVR_E_LENGTH_MISMATCH, "KV-cache contains %d tokens after appending %d", seq_len, q_len);
+      break;
+    }
+    if (!block_tables_host) continue;
+    const int first = (seq_len - q_len) / a->page_size, last = (seq_len - 1) / a->page_size;
+    for (int pi = first; pi <= last; pi++) {
+      const int32_t id = block_tables_host[(int64_t)s * a->max_pages_per_seq + pi];
+      if (id < 0 || id >= a->num_pages) {
+        rc = fail(MVR_E_PAGE_ID, "request %d page %d has id %d outside a pool of %lld pages", s, pi, id,
+                  (long long)a->num_pages);
+        break;
+      }
+      if (page_writable_host && !page_writable_host[id]) {
+        rc = fail(MVR_E_READ_ONLY_PAGE, "cannot mutate written physical page %d", id); // physical_page_pool.rs:197-201
+        break;
+      }
+      if (owner_seen[id]) {
+        rc = fail(MVR_E_INVALID_ARGUMENT, "page %d is written by more than one request", id);
+        break;
+      }
+      owner_seen[id] = 1;
+    }
+  }
+  free(owner_seen);
+  return rc;
+}
 
 size_t mvr_paged_attention_workspace_size(const mvr_paged_attention_args* args) {
   if (check_scalars(args) != MVR_OK) return 0;

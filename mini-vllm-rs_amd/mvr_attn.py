@@ -7,7 +7,12 @@ Mirrors the reference's attention entry points:
   * forward_paged_attention(...)  one request with a PagedCacheLayout, same
                                   arguments and errors as forward_paged_attention
                                   (common.rs:739-817) behind
-                                  forward_cpu_paged_attention (common.rs:426-464).
+                                  forward_cpu_paged_attention (common.rs:426-464);
+  * rope_append(...)              RoPE of the new Q/K rows and the KV-page append
+                                  for every request of a layer (common.rs:294-320,
+                                  kv_cache/paged_cache.rs:290-327);
+  * reconstruct_contiguous(...)   reconstruct_contiguous_tensor
+                                  (kv_cache/paged_cache.rs:363-391).
 Tensors are torch tensors on the GPU; torch supplies device memory and the
 current stream only.  The library must be built (make -C mini-vllm-rs_amd):
 there is no CPU fallback, and a missing library raises.
@@ -33,6 +38,9 @@ MVR_E_PAGES_UNCOVERED = -4
 MVR_E_PAGE_ID = -5
 MVR_E_WORKSPACE = -6
 MVR_E_HIP = -7
+MVR_E_READ_ONLY_PAGE = -8
+
+ROPE_NEOX, ROPE_INTERLEAVED = 0, 1
 
 EXPORTED_SYMBOLS = (
     "mvr_abi_version",
@@ -43,6 +51,8 @@ EXPORTED_SYMBOLS = (
     "mvr_forward_paged_attention",
     "mvr_forward_paged_attention_workspace_size",
     "mvr_reconstruct_contiguous",
+    "mvr_rope_append",
+    "mvr_rope_append_validate",
 )
 
 
@@ -106,6 +116,43 @@ class PagedCacheLayoutC(ctypes.Structure):
     ]
 
 
+class RopeAppendArgs(ctypes.Structure):
+    _fields_ = [
+        ("dtype", ctypes.c_int32),
+        ("rope_type", ctypes.c_int32),
+        ("num_seqs", ctypes.c_int32),
+        ("num_q_heads", ctypes.c_int32),
+        ("num_kv_heads", ctypes.c_int32),
+        ("head_dim", ctypes.c_int32),
+        ("page_size", ctypes.c_int32),
+        ("num_pages", ctypes.c_int64),
+        ("max_pages_per_seq", ctypes.c_int32),
+        ("total_q", ctypes.c_int32),
+        ("max_seq_len", ctypes.c_int32),
+        ("rope_len", ctypes.c_int32),
+        ("q", ctypes.c_void_p),
+        ("q_stride_head", ctypes.c_int64),
+        ("q_stride_token", ctypes.c_int64),
+        ("k", ctypes.c_void_p),
+        ("k_stride_head", ctypes.c_int64),
+        ("k_stride_token", ctypes.c_int64),
+        ("v", ctypes.c_void_p),
+        ("v_stride_head", ctypes.c_int64),
+        ("v_stride_token", ctypes.c_int64),
+        ("cos_table", ctypes.c_void_p),
+        ("sin_table", ctypes.c_void_p),
+        ("block_tables", ctypes.c_void_p),
+        ("seq_lens", ctypes.c_void_p),
+        ("cu_q_lens", ctypes.c_void_p),
+        ("q_out", ctypes.c_void_p),
+        ("q_out_stride_head", ctypes.c_int64),
+        ("q_out_stride_token", ctypes.c_int64),
+        ("key_pool", ctypes.c_void_p),
+        ("value_pool", ctypes.c_void_p),
+        ("stream", ctypes.c_void_p),
+    ]
+
+
 _lib = None
 
 
@@ -141,6 +188,11 @@ def load_library():
     lib.mvr_reconstruct_contiguous.argtypes = [ctypes.c_int32, ctypes.c_void_p, ctypes.c_int64, ctypes.c_int32,
                                                ctypes.c_int32, ctypes.c_int32, ctypes.c_void_p, ctypes.c_int32,
                                                ctypes.c_int32, ctypes.c_void_p, ctypes.c_void_p]
+    lib.mvr_rope_append.restype = ctypes.c_int
+    lib.mvr_rope_append.argtypes = [ctypes.POINTER(RopeAppendArgs)]
+    lib.mvr_rope_append_validate.restype = ctypes.c_int
+    lib.mvr_rope_append_validate.argtypes = [ctypes.POINTER(RopeAppendArgs), ctypes.c_void_p, ctypes.c_void_p,
+                                             ctypes.c_void_p, ctypes.c_void_p]
     if lib.mvr_abi_version() != 1:
         raise RuntimeError("libmvr_attn.so ABI version mismatch")
     _lib = lib
@@ -302,3 +354,75 @@ def reconstruct_contiguous(pool, page_ids, cached_token_count: int, stream=None)
 
 def pages_for(seq_len: int, page_size: int) -> int:
     return math.ceil(seq_len / page_size)
+
+
+def make_rope_append_args(q, k, v, cos_table, sin_table, block_tables, seq_lens, cu_q_lens, key_pool, value_pool,
+                          q_out, *, max_seq_len: int, rope_type: int = ROPE_NEOX, stream=None) -> RopeAppendArgs:
+    """q / q_out [Hq, total_q, D], k / v [Hkv, total_q, D] (unit last stride); cos / sin [rope_len, D/2];
+    pools [num_pages, 1, Hkv, page_size, D]; tables as for paged_attention (seq_lens after the append)."""
+    n_pages, one, hkv, page_size, d = key_pool.shape
+    if one != 1 or value_pool.shape != key_pool.shape:
+        raise MvrError(MVR_E_INVALID_ARGUMENT, "pools must be [num_pages, 1, num_kv_heads, page_size, head_dim]")
+    for t in (q, k, v, q_out):
+        if t.dim() != 3 or t.stride(2) != 1:
+            raise MvrError(MVR_E_INVALID_ARGUMENT, "q, k, v and q_out must be [heads, tokens, head_dim], unit last stride")
+    if not (key_pool.is_contiguous() and value_pool.is_contiguous() and block_tables.is_contiguous()
+            and cos_table.is_contiguous() and sin_table.is_contiguous()):
+        raise MvrError(MVR_E_INVALID_ARGUMENT, "pools, tables and cos/sin must be contiguous")
+    a = RopeAppendArgs()
+    a.dtype = dtype_code(q)
+    a.rope_type = rope_type
+    a.num_seqs = block_tables.shape[0]
+    a.num_q_heads = q.shape[0]
+    a.num_kv_heads = hkv
+    a.head_dim = d
+    a.page_size = page_size
+    a.num_pages = n_pages
+    a.max_pages_per_seq = block_tables.shape[1]
+    a.total_q = q.shape[1]
+    a.max_seq_len = max_seq_len
+    a.rope_len = cos_table.shape[0]
+    a.q, a.q_stride_head, a.q_stride_token = q.data_ptr(), q.stride(0), q.stride(1)
+    a.k, a.k_stride_head, a.k_stride_token = k.data_ptr(), k.stride(0), k.stride(1)
+    a.v, a.v_stride_head, a.v_stride_token = v.data_ptr(), v.stride(0), v.stride(1)
+    a.cos_table = cos_table.data_ptr()
+    a.sin_table = sin_table.data_ptr()
+    a.block_tables = block_tables.data_ptr()
+    a.seq_lens = seq_lens.data_ptr() if seq_lens is not None else None
+    a.cu_q_lens = cu_q_lens.data_ptr() if cu_q_lens is not None else None
+    a.q_out, a.q_out_stride_head, a.q_out_stride_token = q_out.data_ptr(), q_out.stride(0), q_out.stride(1)
+    a.key_pool = key_pool.data_ptr()
+    a.value_pool = value_pool.data_ptr()
+    a.stream = _stream_handle(stream)
+    return a
+
+
+def rope_append(q, k, v, cos_table, sin_table, block_tables, seq_lens, cu_q_lens, key_pool, value_pool, q_out=None,
+                *, max_seq_len: int, rope_type: int = ROPE_NEOX, stream=None):
+    """Rotates q into q_out (a new tensor unless given; may be q itself) and writes the rotated k and v into
+    their page slots; returns q_out."""
+    torch = _torch()
+    if q_out is None:
+        q_out = torch.empty_like(q, memory_format=torch.contiguous_format)
+    a = make_rope_append_args(q, k, v, cos_table, sin_table, block_tables, seq_lens, cu_q_lens, key_pool, value_pool,
+                              q_out, max_seq_len=max_seq_len, rope_type=rope_type, stream=stream)
+    _check(load_library().mvr_rope_append(ctypes.byref(a)))
+    return q_out
+
+
+def validate_rope_append(args: RopeAppendArgs, block_tables_host=None, seq_lens_host=None, cu_q_lens_host=None,
+                         page_writable_host=None) -> None:
+    """Host-side checks of an append's tables (numpy arrays or None); raises MvrError."""
+    import numpy as np
+
+    keep = []
+
+    def ptr(x, dt=np.int32):
+        if x is None:
+            return None
+        x = np.ascontiguousarray(x, dtype=dt)
+        keep.append(x)
+        return x.ctypes.data
+
+    _check(load_library().mvr_rope_append_validate(ctypes.byref(args), ptr(block_tables_host), ptr(seq_lens_host),
+                                                   ptr(cu_q_lens_host), ptr(page_writable_host, np.uint8)))

@@ -189,6 +189,16 @@ CONFIGS = {
 }
 
 
+def rope_tables(head_dim: int, freq_base: float, context_len: int, dtype=np.float16):
+    """cos / sin tables [context_len, head_dim/2] as precompute_rotary_embedding_frequencies builds them
+    (src/models/backends/common.rs:558-577): theta_i = 1 / base^(2i/D) in f32, angle = position * theta_i
+    in f32, cos and sin in f32, then cast to the activation dtype."""
+    i = np.arange(0, head_dim, 2, dtype=np.float32)
+    theta = np.float32(1.0) / np.power(np.float32(freq_base), i / np.float32(head_dim), dtype=np.float32)
+    angle = np.arange(context_len, dtype=np.float32)[:, None] * theta[None, :]
+    return np.cos(angle).astype(dtype), np.sin(angle).astype(dtype)
+
+
 def host_values(w: Workload, chunk: int = 1 << 26):
     """(q, key_pool, value_pool) as numpy arrays in the workload dtype, N(0,1)*scale, from numpy's PCG64."""
     rng = np.random.default_rng(w.seed ^ 0x5EED)

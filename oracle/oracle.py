@@ -1,8 +1,10 @@
 """ORACLE — test infrastructure only.
 
 ctypes binding for liboracle.so, the CPU restatement of mini-vllm-rs page-wise
-attention (src/models/backends/common.rs:739-978).  Imported only by the test
-suite, the smoke check and the benchmark's CPU-baseline leg.
+attention (src/models/backends/common.rs:739-978) and of the RoPE + KV append
+that precedes it (common.rs:294-320, :344-359; kv_cache/paged_cache.rs:290-327;
+kv_cache/physical_page_pool.rs:188-209).  Imported only by the test suite, the
+smoke check and the benchmark's CPU-baseline leg.
 """
 from __future__ import annotations
 
@@ -19,6 +21,10 @@ F32, F16 = 0, 1
 REF_CONCAT_V, REF_PAGEWISE_V, EXACT_F64 = 0, 1, 2
 
 E_INVALID, E_LENGTH, E_UNCOVERED, E_PAGE_ID, E_NO_PAGES, E_ALLOC = -1, -2, -3, -4, -5, -6
+
+ROPE_NEOX, ROPE_INTERLEAVED = 0, 1
+(APPEND_E_INVALID, APPEND_E_EMPTY, APPEND_E_MISSING, APPEND_E_PAGE_ID, APPEND_E_READ_ONLY,
+ APPEND_E_ROPE_RANGE) = -1, -2, -3, -4, -5, -6
 
 
 class OracleDims(ctypes.Structure):
@@ -50,6 +56,40 @@ class OracleBatch(ctypes.Structure):
         ("block_tables", ctypes.c_void_p),
         ("seq_lens", ctypes.c_void_p),
         ("cu_q_lens", ctypes.c_void_p),
+    ]
+
+
+class OracleRopeAppendBatch(ctypes.Structure):
+    _fields_ = [
+        ("dtype", ctypes.c_int),
+        ("rope_type", ctypes.c_int),
+        ("num_seqs", ctypes.c_int),
+        ("num_q_heads", ctypes.c_int),
+        ("num_kv_heads", ctypes.c_int),
+        ("head_dim", ctypes.c_int),
+        ("page_size", ctypes.c_int),
+        ("num_pages", ctypes.c_int64),
+        ("max_pages_per_seq", ctypes.c_int),
+        ("q", ctypes.c_void_p),
+        ("q_stride_head", ctypes.c_int64),
+        ("q_stride_token", ctypes.c_int64),
+        ("k", ctypes.c_void_p),
+        ("k_stride_head", ctypes.c_int64),
+        ("k_stride_token", ctypes.c_int64),
+        ("v", ctypes.c_void_p),
+        ("v_stride_head", ctypes.c_int64),
+        ("v_stride_token", ctypes.c_int64),
+        ("cos_table", ctypes.c_void_p),
+        ("sin_table", ctypes.c_void_p),
+        ("rope_len", ctypes.c_int),
+        ("block_tables", ctypes.c_void_p),
+        ("seq_lens", ctypes.c_void_p),
+        ("cu_q_lens", ctypes.c_void_p),
+        ("q_out", ctypes.c_void_p),
+        ("q_out_stride_head", ctypes.c_int64),
+        ("q_out_stride_token", ctypes.c_int64),
+        ("key_pool", ctypes.c_void_p),
+        ("value_pool", ctypes.c_void_p),
     ]
 
 
@@ -89,6 +129,20 @@ def lib():
         L.oracle_paged_attention.restype = ctypes.c_int
         L.oracle_paged_attention.argtypes = [ctypes.POINTER(OracleBatch), ctypes.c_int, ctypes.c_int, ctypes.c_void_p]
         L.oracle_num_threads.restype = ctypes.c_int
+        L.oracle_rope.restype = ctypes.c_int
+        L.oracle_rope.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_int, ctypes.c_int,
+                                  ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_int,
+                                  ctypes.c_void_p]
+        L.oracle_rope_f64.restype = ctypes.c_int
+        L.oracle_rope_f64.argtypes = L.oracle_rope.argtypes[1:]
+        L.oracle_append_pages.restype = ctypes.c_int
+        L.oracle_append_pages.argtypes = [
+            ctypes.c_size_t, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_int,
+            ctypes.c_int, ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p,
+            ctypes.c_int, ctypes.c_void_p, ctypes.c_char_p, ctypes.c_size_t,
+        ]
+        L.oracle_rope_append.restype = ctypes.c_int
+        L.oracle_rope_append.argtypes = [ctypes.POINTER(OracleRopeAppendBatch), ctypes.c_char_p, ctypes.c_size_t]
         _lib = L
     return _lib
 
@@ -183,3 +237,76 @@ def f32_to_f16_bits(x: float) -> int:
 
 def f16_bits_to_f32(h: int) -> float:
     return lib().oracle_f16_to_f32(h)
+
+
+def rope(x, cos_table, sin_table, start_pos, rope_type=ROPE_NEOX, dtype=F32):
+    """forward_rope for one request: x [heads, q_len, D] in dtype; returns the rotated copy."""
+    npd = _np_dtype(dtype)
+    xa = np.ascontiguousarray(x, dtype=npd)
+    c = np.ascontiguousarray(cos_table, dtype=npd)
+    s = np.ascontiguousarray(sin_table, dtype=npd)
+    heads, q_len, d = xa.shape
+    y = np.empty_like(xa)
+    rc = lib().oracle_rope(dtype, rope_type, _ptr(xa), heads, q_len, d, _ptr(c), _ptr(s), c.shape[0], start_pos,
+                           _ptr(y))
+    if rc != 0:
+        raise OracleError(rc, "rope rejected its input")
+    return y
+
+
+def rope_f64(x, cos_table, sin_table, start_pos, rope_type=ROPE_NEOX):
+    xa = np.ascontiguousarray(x, dtype=np.float64)
+    c = np.ascontiguousarray(cos_table, dtype=np.float64)
+    s = np.ascontiguousarray(sin_table, dtype=np.float64)
+    heads, q_len, d = xa.shape
+    y = np.empty_like(xa)
+    rc = lib().oracle_rope_f64(rope_type, _ptr(xa), heads, q_len, d, _ptr(c), _ptr(s), c.shape[0], start_pos, _ptr(y))
+    if rc != 0:
+        raise OracleError(rc, "rope rejected its input")
+    return y
+
+
+def append_pages(key_pool, value_pool, page_ids, cached_token_count, key, value, page_writable=None):
+    """append_to_pages into numpy pools [N,1,Hkv,P,D] (modified in place); key/value [Hkv, n, D], any dtype."""
+    assert key_pool.flags.c_contiguous and value_pool.flags.c_contiguous
+    assert key_pool.dtype == key.dtype == value.dtype == value_pool.dtype
+    n_pages, _, hkv, page_size, d = key_pool.shape
+    k = np.ascontiguousarray(key)
+    v = np.ascontiguousarray(value)
+    ids = np.ascontiguousarray(page_ids, dtype=np.int64)
+    w = None if page_writable is None else np.ascontiguousarray(page_writable, dtype=np.uint8)
+    err = ctypes.create_string_buffer(256)
+    rc = lib().oracle_append_pages(key_pool.dtype.itemsize, _ptr(key_pool), _ptr(value_pool), n_pages, hkv,
+                                   page_size, d, _ptr(ids) if ids.size else None, ids.size, cached_token_count,
+                                   _ptr(k), _ptr(v), k.shape[1], None if w is None else _ptr(w), err, 256)
+    if rc != 0:
+        raise OracleError(rc, err.value.decode())
+
+
+def rope_append(q, k, v, cos_table, sin_table, block_tables, seq_lens, cu_q_lens, key_pool, value_pool,
+                rope_type=ROPE_NEOX, dtype=F16):
+    """Batched RoPE + append over the library layout: q [Hq, total_q, D], k/v [Hkv, total_q, D].
+    Returns the rotated q; key_pool / value_pool (numpy) are written in place."""
+    npd = _np_dtype(dtype)
+    qa = np.ascontiguousarray(q, dtype=npd)
+    ka = np.ascontiguousarray(k, dtype=npd)
+    va = np.ascontiguousarray(v, dtype=npd)
+    c = np.ascontiguousarray(cos_table, dtype=npd)
+    s = np.ascontiguousarray(sin_table, dtype=npd)
+    bt = np.ascontiguousarray(block_tables, dtype=np.int32)
+    sl = np.ascontiguousarray(seq_lens, dtype=np.int32)
+    cu = np.ascontiguousarray(cu_q_lens, dtype=np.int32)
+    assert key_pool.dtype == npd and value_pool.dtype == npd
+    assert key_pool.flags.c_contiguous and value_pool.flags.c_contiguous
+    hq, total_q, d = qa.shape
+    hkv = ka.shape[0]
+    q_out = np.empty_like(qa)
+    b = OracleRopeAppendBatch(dtype, rope_type, len(sl), hq, hkv, d, key_pool.shape[3], key_pool.shape[0],
+                              bt.shape[1], _ptr(qa), total_q * d, d, _ptr(ka), total_q * d, d, _ptr(va),
+                              total_q * d, d, _ptr(c), _ptr(s), c.shape[0], _ptr(bt), _ptr(sl), _ptr(cu),
+                              _ptr(q_out), total_q * d, d, _ptr(key_pool), _ptr(value_pool))
+    err = ctypes.create_string_buffer(256)
+    rc = lib().oracle_rope_append(ctypes.byref(b), err, 256)
+    if rc != 0:
+        raise OracleError(rc, err.value.decode())
+    return q_out

@@ -139,6 +139,74 @@ def test_reconstruct_contiguous_rejects_like_the_reference():
     assert rc == M.MVR_E_UNSUPPORTED
 
 
+def _rope_args(**kw):
+    a = M.RopeAppendArgs()
+    a.dtype = M.DTYPE_F16
+    a.rope_type = M.ROPE_NEOX
+    a.num_seqs = 2
+    a.num_q_heads = 8
+    a.num_kv_heads = 2
+    a.head_dim = 64
+    a.page_size = 4
+    a.num_pages = 16
+    a.max_pages_per_seq = 4
+    a.total_q = 5
+    a.max_seq_len = 16
+    a.rope_len = 32
+    fake = 1 << 20  # aligned dummy addresses: these calls never launch
+    a.q = a.k = a.v = a.cos_table = a.sin_table = a.block_tables = a.seq_lens = a.cu_q_lens = fake
+    a.q_out = a.key_pool = a.value_pool = fake
+    a.q_stride_head = a.q_out_stride_head = 5 * 64
+    a.k_stride_head = a.v_stride_head = 5 * 64
+    a.q_stride_token = a.q_out_stride_token = a.k_stride_token = a.v_stride_token = 64
+    for k, v in kw.items():
+        setattr(a, k, v)
+    return a
+
+
+@pytest.mark.parametrize("field,value,code,msg", [
+    ("rope_type", 2, M.MVR_E_UNSUPPORTED, "rope_type"),
+    ("head_dim", 60, M.MVR_E_UNSUPPORTED, "head_dim"),
+    ("total_q", 0, M.MVR_E_INVALID_ARGUMENT, "cannot append an empty KV-cache tensor"),
+    ("rope_len", 15, M.MVR_E_INVALID_ARGUMENT, "rotary tables hold 15 positions"),
+    ("max_pages_per_seq", 3, M.MVR_E_PAGES_UNCOVERED, "cannot hold 16 tokens"),
+    ("k", 4 + (1 << 20), M.MVR_E_INVALID_ARGUMENT, "aligned"),
+    ("v_stride_token", 66, M.MVR_E_INVALID_ARGUMENT, "multiples of 4"),
+    ("cu_q_lens", None, M.MVR_E_INVALID_ARGUMENT, "required"),
+])
+def test_rope_append_scalar_checks_reject_before_launch(field, value, code, msg):
+    lib = M.load_library()
+    rc = lib.mvr_rope_append(ctypes.byref(_rope_args(**{field: value})))
+    assert rc == code
+    assert msg in lib.mvr_last_error().decode()
+
+
+def test_rope_append_validate_mirrors_reference_errors():
+    a = _rope_args()
+    bt = [[3, 7, 1, 0], [9, 2, 0, 0]]
+    writable = [1] * 16
+    M.validate_rope_append(a, bt, [10, 6], [0, 3, 5], writable)  # positions 7..9 and 4..5
+    with pytest.raises(M.MvrError, match="cannot append an empty KV-cache tensor"):
+        M.validate_rope_append(a, bt, [10, 6], [0, 5, 5])
+    w = list(writable)
+    w[1] = 0  # page 1 holds positions 8..9 of request 0: written and shared
+    with pytest.raises(M.MvrError, match="cannot mutate written physical page 1") as e:
+        M.validate_rope_append(a, bt, [10, 6], [0, 3, 5], w)
+    assert e.value.code == M.MVR_E_READ_ONLY_PAGE
+    w = list(writable)
+    w[3] = 0  # page 3 holds positions 0..3: not written by this append
+    M.validate_rope_append(a, bt, [10, 6], [0, 3, 5], w)
+    with pytest.raises(M.MvrError, match="written by more than one request"):
+        M.validate_rope_append(a, [[3, 7, 2, 0], [9, 2, 0, 0]], [10, 6], [0, 3, 5])
+    with pytest.raises(M.MvrError, match="outside a pool of 16 pages") as e:
+        M.validate_rope_append(a, [[3, 7, 99, 0], [9, 2, 0, 0]], [10, 6], [0, 3, 5])
+    assert e.value.code == M.MVR_E_PAGE_ID
+    with pytest.raises(M.MvrError, match="after appending"):
+        M.validate_rope_append(a, bt, [2, 6], [0, 3, 5])
+    with pytest.raises(M.MvrError, match="total_q"):
+        M.validate_rope_append(a, bt, [10, 6], [0, 3, 4])
+
+
 def test_workloads_match_stated_sizes():
     import workloads as W
 
