@@ -129,6 +129,50 @@ def measure(W, M, torch, cfg, steps, warmup):
     return res
 
 
+class AppendRunner:
+    """RoPE + KV-page append for the new tokens of a workload (its block tables and pools), prebuilt args."""
+
+    def __init__(self, w, tensors, torch, M, W):
+        import numpy as np
+
+        g = torch.Generator(device="cuda").manual_seed(w.seed)
+        T, d = w.total_q, w.head_dim
+        dt = torch.float16 if w.dtype == "f16" else torch.float32
+        self.q = (torch.randn((w.num_q_heads, T, d), generator=g, device="cuda") * 0.3).to(dt)
+        self.k = (torch.randn((w.num_kv_heads, T, d), generator=g, device="cuda") * 0.3).to(dt)
+        self.v = (torch.randn((w.num_kv_heads, T, d), generator=g, device="cuda") * 0.3).to(dt)
+        cos, sin = W.rope_tables(d, 10000.0, w.max_seq_len, np.float16 if w.dtype == "f16" else np.float32)
+        self.cos, self.sin = torch.from_numpy(cos).cuda(), torch.from_numpy(sin).cuda()
+        self.q_out = torch.empty_like(self.q)
+        self.args = M.make_rope_append_args(self.q, self.k, self.v, self.cos, self.sin, tensors["block_tables"],
+                                            tensors["seq_lens"], tensors["cu_q_lens"], tensors["key_pool"],
+                                            tensors["value_pool"], self.q_out, max_seq_len=w.max_seq_len)
+        self.lib = M.load_library()
+        self.M = M
+        es = 2 if w.dtype == "f16" else 4
+        # Q read + written, K read + written, V read + written, one cos and one sin row, one page id per token.
+        self.bytes = T * ((w.num_q_heads + 2 * w.num_kv_heads) * d * es * 2 + d * es + 4)
+
+    def step(self):
+        rc = self.lib.mvr_rope_append(ctypes.byref(self.args))
+        if rc != 0:
+            raise self.M.MvrError(rc, self.lib.mvr_last_error().decode())
+
+
+def measure_append(W, M, torch, cfg, steps, warmup):
+    w = W.CONFIGS[cfg]()
+    t = W.device_tensors(w, None)
+    r = AppendRunner(w, t, torch, M, W)
+    wall, per = time_steps(r, torch, steps, warmup)
+    med = per[len(per) // 2]
+    res = dict(workload=f"rope+append of the new tokens of {w.name} ({w.total_q} tokens)",
+               us_per_step_median=round(med, 2), bytes=r.bytes,
+               eff_gbs=round(r.bytes / (med * 1e-6) / 1e9, 1), hbm_frac=round(r.bytes / (med * 1e-6) / 1e9 / HBM_PEAK_GBS, 4))
+    del t, r
+    torch.cuda.empty_cache()
+    return res
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -217,6 +261,10 @@ def main():
             log(f"[bench] config {cfg}")
             per_cfg[str(cfg)] = measure(W, M, torch, cfg, max(20, a.steps // 2), a.warmup)
         result["configs"] = per_cfg
+        result["rope_append"] = {}
+        for cfg in (3, 4):
+            log(f"[bench] rope+append, config {cfg}")
+            result["rope_append"][str(cfg)] = measure_append(W, M, torch, cfg, max(20, a.steps // 2), a.warmup)
     if not a.skip_cpu:
         log("[bench] cpu baseline")
         result["cpu_baseline"] = cpu_baseline(W)
