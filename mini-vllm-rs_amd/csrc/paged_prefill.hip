@@ -26,6 +26,8 @@
 
 #include <math.h>
 
+#include <type_traits>
+
 namespace mvr {
 namespace {
 
@@ -37,6 +39,7 @@ typedef float float4v __attribute__((ext_vector_type(4)));
 typedef float float16v __attribute__((ext_vector_type(16)));
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) short4v lds_short4;
+typedef __attribute__((address_space(3))) void lds_void;
 typedef __attribute__((address_space(4))) int32_t const_i32;
 
 constexpr int kTileTokens = 32;
@@ -44,18 +47,34 @@ constexpr int kRowsPerWave = 32;
 constexpr int kWaves = 4;
 constexpr int kBlockRows = kRowsPerWave * kWaves;
 constexpr int kXcds = 8;
+constexpr int kStages = 4; // LDS stages; a power of two so the unrolled loop names each statically
 constexpr float kRescaleThreshold = 8.0f; // log2 units: p <= 2^8 between rescales
 
 struct SeqRows {
   int seq_len, q_start, q_len;
 };
 
-// Block barrier that orders LDS only.  __syncthreads() also waits for every
-// outstanding global load (vmcnt(0)), which would stall on the tiles being
-// prefetched into registers; those are consumed later through ordinary
-// register dependencies, so the barrier only needs this block's LDS writes
-// to have landed.
-__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+// Tile barrier: waits until at most kNewer of this wavefront's direct-to-LDS
+// tile loads are in flight and its LDS reads have returned, then meets the
+// other wavefronts.  (__syncthreads() would wait for every load, vmcnt(0),
+// and drain the prefetch.)  The wait is the compiler's own s_waitcnt, so its
+// bookkeeping of the direct-to-LDS loads stays exact; the empty asm
+// statements keep memory accesses from moving across the barrier without
+// any further wait.
+// 16 bytes per lane from global memory straight into LDS at lds + 16 * lane
+// (global_load_lds_dwordx4).  A plain __device__ function: lambdas in kernels
+// are also compiled for the host, where this gfx950 builtin does not exist.
+__device__ __forceinline__ void load_to_lds16(const void* src, void* lds) {
+  __builtin_amdgcn_global_load_lds(src, (lds_void*)lds, 16, 0, 0);
+}
+
+template <int kNewer>
+__device__ __forceinline__ void tile_barrier() {
+  __builtin_amdgcn_s_waitcnt((kNewer & 0xF) | ((kNewer >> 4) << 14) | (0x7 << 4)); // vmcnt(n) expcnt(7) lgkmcnt(0)
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
 
 __device__ __forceinline__ SeqRows load_rows(const PrefillParams& p, int b) {
   SeqRows s;
@@ -98,10 +117,15 @@ struct Tile {
 };
 
 template <int D>
-__global__ __launch_bounds__(kWaves * 64, 2) void paged_prefill_kernel(PrefillParams p) {
+__global__ __launch_bounds__(kWaves * 64, D == 128 ? 1 : 2) void paged_prefill_kernel(PrefillParams p) {
   typedef Tile<D> TL;
-  __shared__ __attribute__((aligned(16))) half_t k_lds[3][TL::kElems];
-  __shared__ __attribute__((aligned(16))) half_t v_lds[3][TL::kElems];
+  // One LDS object per stage and operand: the compiler tracks the
+  // direct-to-LDS loads per object, so a read of one stage never waits for
+  // the loads still landing in another.
+  __shared__ __attribute__((aligned(16))) half_t k_lds0[TL::kElems], k_lds1[TL::kElems], k_lds2[TL::kElems],
+      k_lds3[TL::kElems];
+  __shared__ __attribute__((aligned(16))) half_t v_lds0[TL::kElems], v_lds1[TL::kElems], v_lds2[TL::kElems],
+      v_lds3[TL::kElems];
 
   const int tid = threadIdx.x;
   const int l = tid & 63;
@@ -178,69 +202,57 @@ __global__ __launch_bounds__(kWaves * 64, 2) void paged_prefill_kernel(PrefillPa
   auto page_div = [&](int tok) { return tok >> pshift; };
   auto page_mod = [&](int tok) { return tok & (p.page_size - 1); };
 
-  // Cooperative tile load: thread tid moves chunks ci = tid + 256u of K and V.
-  // The tokens one wavefront moves for a given u are 4 (D=128) or 8 (D=64)
-  // consecutive tokens inside a 16-token group, hence inside one page.
-  // Loop-invariant parts (token row, column, LDS slots) are computed once.
-  int ld_t[TL::kChunksPerThread], ld_c8[TL::kChunksPerThread], ld_t0[TL::kChunksPerThread];
-  int st_k[TL::kChunksPerThread], st_v[TL::kChunksPerThread];
+  // Tiles move straight from HBM/L2 into LDS (global_load_lds_dwordx4: lane
+  // i of a wavefront writes 16 bytes at the wavefront's LDS base + 16 i), so
+  // they take no registers and no LDS store instructions.  Wavefront w, step
+  // u fills LDS chunks (u*4 + w)*64 .. +63 of a tile; LDS chunk P holds token
+  // row t = P / (D/8), physical chunk P % (D/8), and the lane fetches the
+  // logical 16-byte chunk that the K or V swizzle puts there.  The tokens of
+  // one (w, u) are 4 (D=128) or 8 (D=64) consecutive tokens of a 16-token
+  // group, hence of one page: one scalar block-table load per (w, u).
+  int ld_t[TL::kChunksPerThread], ld_t0[TL::kChunksPerThread], ld_k[TL::kChunksPerThread],
+      ld_v[TL::kChunksPerThread];
 #pragma unroll
   for (int u = 0; u < TL::kChunksPerThread; u++) {
-    const int ci = tid + kWaves * 64 * u;
-    const int t = ci / TL::kChunksPerRow, c = ci % TL::kChunksPerRow;
+    const int P = (u * kWaves + wave) * 64 + l;
+    const int t = P / TL::kChunksPerRow, cs = P % TL::kChunksPerRow;
     ld_t[u] = t;
-    ld_c8[u] = 8 * c;
-    ld_t0[u] = (wave * 64 + kWaves * 64 * u) / TL::kChunksPerRow;
-    st_k[u] = t * D + 8 * (c ^ TL::kswz(t));
-    st_v[u] = t * D + ((c >> 1) ^ TL::vswz(t)) * 16 + (c & 1) * 8;
+    ld_t0[u] = (u * kWaves + wave) * 64 / TL::kChunksPerRow;
+    ld_k[u] = 8 * (cs ^ TL::kswz(t));
+    ld_v[u] = 8 * (2 * ((cs >> 1) ^ TL::vswz(t)) + (cs & 1));
   }
-  // Branch-free: tokens past the sequence end read the last valid slot of the
-  // same page and are zeroed when stored, so the loads carry no control flow
-  // and the compiler can count outstanding loads exactly.
-  typedef u32x4 Regs[TL::kChunksPerThread];
-  auto load_tile = [&](int j, Regs& kr, Regs& vr) {
+  // Branch-free: tokens past the sequence end re-read the last valid token,
+  // so every tile issues the same loads.  Those duplicate keys lie past every
+  // row's causal limit (the last tile is a diagonal tile for every wavefront
+  // that sees it), so their scores are masked to -inf, p = 0, and
+  // p * (finite duplicate V) = 0.
+  // Block-table entries of a tile's (w, u) groups, read one iteration before
+  // the tile's loads are issued: a scalar load makes its user wait for
+  // lgkmcnt(0), which would also drain every LDS read in flight, so the
+  // entries are fetched just before a barrier, where lgkmcnt is drained anyway.
+  struct Pages {
+    int64_t pg[TL::kChunksPerThread];
+  };
+  auto fetch_pages = [&](int j) {
+    Pages r;
+#pragma unroll
+    for (int u = 0; u < TL::kChunksPerThread; u++)
+      r.pg[u] = bt[page_div(min(j * kTileTokens + ld_t0[u], s.seq_len - 1))]; // wave-uniform: scalar load
+    return r;
+  };
+  auto issue_tile = [&](int j, const Pages& pages, half_t* kb, half_t* vb) {
 #pragma unroll
     for (int u = 0; u < TL::kChunksPerThread; u++) {
       const int tg = min(j * kTileTokens + ld_t[u], s.seq_len - 1);
-      const int tg0 = min(j * kTileTokens + ld_t0[u], s.seq_len - 1);
-      const int64_t page = bt[page_div(tg0)]; // wave-uniform index: scalar load
-      const int64_t off = ((page * p.num_kv_heads + h) * p.page_size + page_mod(tg)) * D + ld_c8[u];
-      kr[u] = *reinterpret_cast<const u32x4*>(kpool + off);
-      vr[u] = *reinterpret_cast<const u32x4*>(vpool + off);
+      const int64_t row = ((pages.pg[u] * p.num_kv_heads + h) * p.page_size + page_mod(tg)) * D;
+      const int dst = (u * kWaves + wave) * 64 * 8;
+      load_to_lds16(kpool + row + ld_k[u], kb + dst);
+      load_to_lds16(vpool + row + ld_v[u], vb + dst);
     }
   };
-  auto store_tile = [&](int j, const Regs& kr, const Regs& vr, int buf) {
-    half_t* kb = k_lds[buf];
-    half_t* vb = v_lds[buf];
-    if ((j + 1) * kTileTokens <= s.seq_len) { // whole tile inside the sequence (block-uniform)
-#pragma unroll
-      for (int u = 0; u < TL::kChunksPerThread; u++) {
-        *reinterpret_cast<u32x4*>(kb + st_k[u]) = kr[u];
-        *reinterpret_cast<u32x4*>(vb + st_v[u]) = vr[u];
-      }
-    } else {
-#pragma unroll
-      for (int u = 0; u < TL::kChunksPerThread; u++) {
-        const bool in_seq = j * kTileTokens + ld_t[u] < s.seq_len;
-        const u32x4 zero = {0u, 0u, 0u, 0u};
-        *reinterpret_cast<u32x4*>(kb + st_k[u]) = in_seq ? kr[u] : zero;
-        *reinterpret_cast<u32x4*>(vb + st_v[u]) = in_seq ? vr[u] : zero;
-      }
-    }
-  };
-
-  // Pipeline: 3 LDS stages and 2 register sets.  Iteration k issues the loads
-  // of tile k+2, computes tile k from stage k%3 and stores tile k+1 (loaded
-  // one iteration earlier) into stage (k+1)%3, so every load has two
-  // iterations of math to arrive.  Loads past the last tile re-read it
-  // (clamped index) and stores past it land in a stage nobody reads again:
-  // no branch around any load, so the outstanding-load count is exact.
-  Regs k0r, v0r, k1r, v1r;
-  const int j_last = max(j1 - 1, j0);
-  load_tile(j0, k0r, v0r);
-  load_tile(min(j0 + 1, j_last), k1r, v1r);
-  store_tile(j0, k0r, v0r, 0);
-  lds_barrier();
+  constexpr int kLoadsPerTile = 2 * TL::kChunksPerThread; // per lane
+  half_t* const k_st[kStages] = {k_lds0, k_lds1, k_lds2, k_lds3};
+  half_t* const v_st[kStages] = {v_lds0, v_lds1, v_lds2, v_lds3};
 
   // Per-lane LDS read offsets, loop-invariant.  K: lane reads token l%32,
   // chunk 2s+hh.  V^T: step u reads rows 16u+4hh+rsub (and +8), 16 columns
@@ -267,81 +279,181 @@ __global__ __launch_bounds__(kWaves * 64, 2) void paged_prefill_kernel(PrefillPa
   }
   const float sl2 = p.scale_log2;
 
-  auto compute_tile = [&](int j, int buf) {
-    const int tok0 = j * kTileTokens;
-    // Skip the math when every row of this wave is causally past the tile.
-    if (tok0 <= wave_limit) {
-      const half_t* kb = k_lds[buf];
-      const half_t* vb = v_lds[buf];
-      float16v sc;
+  // Wave-uniform tile predicates: a tile is visible when some row of this
+  // wavefront sees its first key, and diagonal when some row does not see
+  // its last key (then scores are masked).
+  auto visible = [&](int j) { return j < j1 && j * kTileTokens <= wave_limit; };
+  auto diagonal = [&](int j) { return j * kTileTokens + kTileTokens - 1 > wave_min_limit; };
+
+  // S^T of the tile in stage buf: D/16 MFMAs, K read straight into the A operand.
+  auto qk = [&](const half_t* kb) {
+    float16v acc;
 #pragma unroll
-      for (int e = 0; e < 16; e++) sc[e] = 0.f;
+    for (int e = 0; e < 16; e++) acc[e] = 0.f;
 #pragma unroll
-      for (int st = 0; st < D / 16; st++) {
-        const half8 ka = *reinterpret_cast<const half8*>(kb + rk[st]);
-        sc = __builtin_amdgcn_mfma_f32_32x32x16_f16(ka, q[st], sc, 0, 0, 0);
-      }
-      // Lane holds tokens tok0 + 8*(e/4) + 4*hh + e%4 of row rho (unscaled).
-      if (tok0 + kTileTokens - 1 > wave_min_limit) { // causal diagonal: mask (wave-uniform)
+    for (int st = 0; st < D / 16; st++)
+      acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(*reinterpret_cast<const half8*>(kb + rk[st]), q[st], acc, 0, 0, 0);
+    return acc;
+  };
+  // Lane holds tokens tok0 + 8*(e/4) + 4*hh + e%4 of row rho.
+  auto mask = [&](int j, float16v& sv) {
+    const int rel = limit - j * kTileTokens - 4 * hh;
 #pragma unroll
-        for (int e = 0; e < 16; e++) {
-          const int tok = tok0 + 8 * (e >> 2) + 4 * hh + (e & 3);
-          sc[e] = tok <= limit ? sc[e] : -INFINITY;
-        }
-      }
-      float mx = fmaxf(fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3])), fmaxf(fmaxf(sc[4], sc[5]), fmaxf(sc[6], sc[7])));
-      mx = fmaxf(mx, fmaxf(fmaxf(fmaxf(sc[8], sc[9]), fmaxf(sc[10], sc[11])),
-                           fmaxf(fmaxf(sc[12], sc[13]), fmaxf(sc[14], sc[15]))));
-      mx *= sl2; // log2 units (scale > 0 keeps the order)
-      mx = fmaxf(mx, __shfl_xor(mx, 32));
-      const bool grow = mx > m + kRescaleThreshold || (m == -INFINITY && mx != -INFINITY);
-      if (__any(grow)) {
-        const float m_new = grow ? mx : m;
-        const float alpha = m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m - m_new);
+    for (int e = 0; e < 16; e++) sv[e] = 8 * (e >> 2) + (e & 3) <= rel ? sv[e] : -INFINITY;
+  };
+  // Scaled row max (log2 units; scale > 0 keeps the order), both lane halves.
+  auto row_max = [&](const float16v& sv) {
+    float a = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
+    float b = fmaxf(fmaxf(sv[4], sv[5]), fmaxf(sv[6], sv[7]));
+    float c = fmaxf(fmaxf(sv[8], sv[9]), fmaxf(sv[10], sv[11]));
+    float d = fmaxf(fmaxf(sv[12], sv[13]), fmaxf(sv[14], sv[15]));
+    const float mx = fmaxf(fmaxf(a, b), fmaxf(c, d)) * sl2;
+    const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
+    return fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
+  };
+  // Lazy rescale: the running max only moves (and O is only rescaled) when a
+  // score exceeds it by more than 2^8, so P stays <= 2^8 in f16.
+  auto advance_max = [&](float mx) {
+    const bool grow = mx > m + kRescaleThreshold || (m == -INFINITY && mx != -INFINITY);
+    if (__any(grow)) {
+      const float m_new = grow ? mx : m;
+      const float alpha = m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m - m_new);
 #pragma unroll
-        for (int n = 0; n < D / 32; n++) o[n] *= alpha;
-        lsum *= alpha;
-        m = m_new;
-      }
-      const float neg_m = m == -INFINITY ? 0.f : -m;
-      half8 pb[2];
-      float psum = 0.f;
+      for (int n = 0; n < D / 32; n++) o[n] *= alpha;
+      lsum *= alpha;
+      m = m_new;
+    }
+  };
+  // P = 2^(s*scale_log2 - m) in f16 (masked keys give 2^-inf = 0) and its row sum.
+  auto exps = [&](const float16v& sv, half8 (&pb)[2]) {
+    const float neg_m = m == -INFINITY ? 0.f : -m;
+    float psum = 0.f;
 #pragma unroll
-      for (int e = 0; e < 16; e++) {
-        const float pe = __builtin_amdgcn_exp2f(fmaf(sc[e], sl2, neg_m)); // <= 2^8; masked: exp2(-inf) = 0
-        psum += pe;
-        pb[e >> 3][e & 7] = (half_t)pe;
-      }
-      lsum += psum;
-      // O^T += V^T P^T over two 16-token steps u; step u uses tokens
-      // 16u + 4*hh + {0..3} and 16u + 8 + 4*hh + {0..3} (the ones this lane holds).
+    for (int e = 0; e < 16; e++) {
+      const float pe = __builtin_amdgcn_exp2f(fmaf(sv[e], sl2, neg_m));
+      psum += pe;
+      pb[e >> 3][e & 7] = (half_t)pe;
+    }
+    lsum += psum;
+  };
+  // O^T += V^T P^T over two 16-token steps u; step u uses tokens
+  // 16u + 4*hh + {0..3} and 16u + 8 + 4*hh + {0..3} (the ones this lane holds).
+  auto pv = [&](const half_t* vb, const half8 (&pb)[2]) {
 #pragma unroll
-      for (int n = 0; n < D / 32; n++) {
+    for (int n = 0; n < D / 32; n++) {
 #pragma unroll
-        for (int u = 0; u < 2; u++) {
-          const short4v ra = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4*)(vb + rva[n][u]));
-          const short4v rb = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4*)(vb + rvb[n][u]));
-          const half8 vt = __builtin_bit_cast(half8, __builtin_shufflevector(ra, rb, 0, 1, 2, 3, 4, 5, 6, 7));
-          o[n] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vt, pb[u], o[n], 0, 0, 0);
-        }
+      for (int u = 0; u < 2; u++) {
+        const short4v ra = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4*)(vb + rva[n][u]));
+        const short4v rb = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4*)(vb + rvb[n][u]));
+        const half8 vt = __builtin_bit_cast(half8, __builtin_shufflevector(ra, rb, 0, 1, 2, 3, 4, 5, 6, 7));
+        o[n] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vt, pb[u], o[n], 0, 0, 0);
       }
     }
   };
 
-  // Unrolled by two so that each register set is named statically.
-  for (int j = j0, stage = 0; j < j1; j += 2) {
-    load_tile(min(j + 2, j_last), k0r, v0r);
-    compute_tile(j, stage);
-    stage = stage == 2 ? 0 : stage + 1;
-    store_tile(j + 1, k1r, v1r, stage);
-    lds_barrier();
-    if (j + 1 >= j1) break;
-    load_tile(min(j + 3, j_last), k1r, v1r);
-    compute_tile(j + 1, stage);
-    stage = stage == 2 ? 0 : stage + 1;
-    store_tile(j + 2, k0r, v0r, stage);
-    lds_barrier();
+  // Software pipeline over 32-token tiles in kStages LDS stages; the stage of
+  // tile t is (t - j0) % kStages.  Iteration j issues the loads of tile j+3
+  // into the stage that held tile j-1 (released by the previous barrier),
+  // then, with tile j's scores sc already masked and folded into the running
+  // max:
+  //   block A: S(j+1) = K(j+1) Q^T on the MFMA pipe while the VALU computes
+  //            P(j) = exp2(sc - m) (independent instructions, one basic block);
+  //   block B: O += V(j)^T P(j) on the MFMA pipe while the VALU masks and
+  //            reduces S(j+1);
+  // moves the running max for tile j+1 and waits for tile j+2 (loads issued
+  // one iteration earlier) before the barrier.  Loads past the last tile
+  // re-read it (clamped) into stages nobody reads again.
+  const int j_last = max(j1 - 1, j0);
+  constexpr std::integral_constant<int, 0> c0{};
+  constexpr std::integral_constant<int, 1> c1{};
+  constexpr std::integral_constant<int, 2> c2{};
+  issue_tile(j0, fetch_pages(j0), k_st[0], v_st[0]);
+  issue_tile(min(j0 + 1, j_last), fetch_pages(min(j0 + 1, j_last)), k_st[1], v_st[1]);
+  issue_tile(min(j0 + 2, j_last), fetch_pages(min(j0 + 2, j_last)), k_st[2], v_st[2]);
+  Pages next_pages = fetch_pages(min(j0 + 3, j_last));
+  tile_barrier<kLoadsPerTile>(); // tiles j0, j0+1 landed
+
+  float16v sc;
+#pragma unroll
+  for (int e = 0; e < 16; e++) sc[e] = 0.f;
+  if (visible(j0)) {
+    sc = qk(k_st[0]);
+    if (diagonal(j0)) mask(j0, sc);
+    advance_max(row_max(sc));
   }
+
+  // Tiles every row of the block sees in full need neither visibility tests
+  // nor masks; while tiles j and j+1 are both such, an iteration is one
+  // branch-free stretch the scheduler can interleave (MFMA chains under the
+  // softmax VALU work).
+  auto iterate_clear = [&](int j, auto st_c) {
+    constexpr int st = decltype(st_c)::value;
+    issue_tile(min(j + 3, j_last), next_pages, k_st[(st + 3) & (kStages - 1)],
+               v_st[(st + 3) & (kStages - 1)]);
+    half8 pb[2];
+    const float16v sn = qk(k_st[(st + 1) & (kStages - 1)]);
+    exps(sc, pb);
+    pv(v_st[st], pb);
+    advance_max(row_max(sn));
+    sc = sn;
+    next_pages = fetch_pages(min(j + 4, j_last));
+    tile_barrier<kLoadsPerTile>();
+  };
+  auto iterate = [&](int j, auto st_c) {
+    constexpr int st = decltype(st_c)::value;
+    issue_tile(min(j + 3, j_last), next_pages, k_st[(st + 3) & (kStages - 1)],
+               v_st[(st + 3) & (kStages - 1)]);
+    if (visible(j)) {
+      half8 pb[2];
+      if (visible(j + 1)) {
+        float16v sn = qk(k_st[(st + 1) & (kStages - 1)]); // block A
+        exps(sc, pb);
+        if (diagonal(j + 1)) mask(j + 1, sn);
+        pv(v_st[st], pb); // block B
+        advance_max(row_max(sn));
+        sc = sn;
+      } else {
+        exps(sc, pb);
+        pv(v_st[st], pb);
+      }
+    }
+    next_pages = fetch_pages(min(j + 4, j_last));
+    tile_barrier<kLoadsPerTile>();
+  };
+  // Smallest causal limit among the block's valid rows.
+  int block_min_limit;
+  {
+    const int rho0 = rt * kBlockRows;
+    const int rho_last = min(rho0 + kBlockRows, rows) - 1;
+    const int min_i = rho0 / s.q_len != rho_last / s.q_len ? 0 : rho0 % s.q_len;
+    block_min_limit = s.seq_len - s.q_len + min_i;
+  }
+  const int clear_tiles = min(j1, (block_min_limit + 1) / kTileTokens); // tiles j < this are clear
+  // Clear iterations need j + 1 clear as well; their count is a multiple of
+  // kStages so that the general loop starts on stage 0.
+  const int j_mid = j0 + max(0, (clear_tiles - 1 - j0) / kStages * kStages);
+
+  // Unrolled by kStages so that every stage is named statically: LDS
+  // addresses become immediate offsets and each stage is its own object.
+  constexpr std::integral_constant<int, 3> c3{};
+  for (int j = j0; j < j_mid; j += kStages) {
+    iterate_clear(j, c0);
+    iterate_clear(j + 1, c1);
+    iterate_clear(j + 2, c2);
+    iterate_clear(j + 3, c3);
+  }
+  for (int j = j_mid; j < j1; j += kStages) {
+    iterate(j, c0);
+    if (j + 1 >= j1) break;
+    iterate(j + 1, c1);
+    if (j + 2 >= j1) break;
+    iterate(j + 2, c2);
+    if (j + 3 >= j1) break;
+    iterate(j + 3, c3);
+  }
+  // Every issued load has landed before the block exits (the last barrier
+  // left up to one tile of clamped re-reads in flight).
+  __builtin_amdgcn_s_waitcnt(0x0070); // vmcnt(0) expcnt(7) lgkmcnt(0)
 
   const float ltot = lsum + __shfl_xor(lsum, 32);
   // Lane holds O^T[d][rho] for d = 32n + 8*(e/4) + 4*hh + e%4.
