@@ -159,6 +159,41 @@ class AppendRunner:
             raise self.M.MvrError(rc, self.lib.mvr_last_error().decode())
 
 
+class CascadeRunner(Runner):
+    """The workload's call through mvr_paged_attention_cascade with its prefix groups."""
+
+    def __init__(self, w, tensors, torch, M, W):
+        super().__init__(w, tensors, torch, M)
+        gcu, gpre, gbt, spre = W.cascade_tables(w)
+        self.dev = [torch.from_numpy(x).cuda() for x in (gcu, gpre, gbt, spre)]
+        self.groups = M.make_cascade_groups(*self.dev, max_group_q_len=int(max(gcu[1:] - gcu[:-1])),
+                                            max_prefix_len=int(gpre.max()), sum_prefix_lens=int(spre.sum()))
+        need = self.lib.mvr_paged_attention_cascade_workspace_size(ctypes.byref(self.args), ctypes.byref(self.groups))
+        self.ws = M.new_workspace(need, "cuda")
+        self.args.workspace = self.ws.data_ptr()
+        self.args.workspace_bytes = need
+
+    def step(self):
+        rc = self.lib.mvr_paged_attention_cascade(ctypes.byref(self.args), ctypes.byref(self.groups))
+        if rc != 0:
+            raise self.M.MvrError(rc, self.lib.mvr_last_error().decode())
+
+
+def measure_cascade(W, M, torch, cfg, steps, warmup):
+    w = W.CONFIGS[cfg]()
+    t = W.device_tensors(w, None)
+    r = CascadeRunner(w, t, torch, M, W)
+    wall, per = time_steps(r, torch, steps, warmup)
+    med = per[len(per) // 2]
+    ub = w.algorithmic_bytes(unique=True)
+    res = dict(workload=f"{w.name} through cascade attention ({len(w.prefix_groups)} prefix groups)",
+               us_per_step_median=round(med, 2), unique_bytes=ub, unique_gbs=round(ub / (med * 1e-6) / 1e9, 1),
+               hbm_frac=round(ub / (med * 1e-6) / 1e9 / HBM_PEAK_GBS, 4))
+    del t, r
+    torch.cuda.empty_cache()
+    return res
+
+
 def measure_append(W, M, torch, cfg, steps, warmup):
     w = W.CONFIGS[cfg]()
     t = W.device_tensors(w, None)
@@ -261,6 +296,8 @@ def main():
             log(f"[bench] config {cfg}")
             per_cfg[str(cfg)] = measure(W, M, torch, cfg, max(20, a.steps // 2), a.warmup)
         result["configs"] = per_cfg
+        log("[bench] config 5 through cascade attention")
+        result["cascade"] = {"5": measure_cascade(W, M, torch, 5, max(20, a.steps // 2), a.warmup)}
         result["rope_append"] = {}
         for cfg in (3, 4):
             log(f"[bench] rope+append, config {cfg}")

@@ -117,6 +117,51 @@ int mvr_paged_attention(const mvr_paged_attention_args* args);
 int mvr_paged_attention_validate(const mvr_paged_attention_args* args, const int32_t* block_tables_host,
                                  const int32_t* seq_lens_host, const int32_t* cu_q_lens_host);
 
+/* Prefix sharing (cascade attention).  Requests whose block tables start
+   with the same physical pages (a cached prefix adopted from the prefix
+   index, kv_cache/prefix_index.rs:174-211, request_state.rs:92-103) form a
+   group; the members of a group are consecutive sequences of the batch.
+   The shared prefix is attended once per group, by all members' query rows
+   together, instead of once per member; each member's remaining keys are
+   attended separately and the two results are merged exactly (log-sum-exp
+   weights).  Groups cover the first sequences of the batch in order (group
+   g holds the consecutive sequences whose packed tokens span
+   group_cu_q_lens[g] .. group_cu_q_lens[g+1]); a group may have prefix 0
+   (its members share nothing), and sequences after the last group have no
+   prefix. */
+typedef struct mvr_cascade_groups {
+  int32_t num_groups;
+  int32_t max_group_q_len;           /* >= every group's packed query tokens */
+  int32_t max_prefix_len;            /* >= every group's prefix tokens */
+  const int32_t* group_cu_q_lens;    /* device [num_groups + 1]: packed-token range of each group's members */
+  const int32_t* group_prefix_lens;  /* device [num_groups]: shared tokens, a multiple of page_size (0 allowed)
+                                        and <= every member's cached_kv_len */
+  const int32_t* group_block_tables; /* device [num_groups, max_pages_per_seq]: the shared pages */
+  const int32_t* seq_prefix_lens;    /* device [num_seqs]: prefix tokens of the sequence's group, 0 if none */
+  int64_t sum_prefix_lens;           /* optional planning hint: sum of seq_prefix_lens (0 = unknown) */
+} mvr_cascade_groups;
+
+/* Workspace for mvr_paged_attention_cascade (no initialisation needed). */
+size_t mvr_paged_attention_cascade_workspace_size(const mvr_paged_attention_args* args,
+                                                  const mvr_cascade_groups* groups);
+
+/* mvr_paged_attention with shared prefixes read once per group.  Same
+   arguments, output and numerics (an exact split of the softmax sum; results
+   differ from the plain call only by rounding).  Stream-ordered, allocates
+   nothing. */
+int mvr_paged_attention_cascade(const mvr_paged_attention_args* args, const mvr_cascade_groups* groups);
+
+/* Host-side checks of the group tables: members consecutive and aligned with
+   cu_q_lens, prefix lengths page-aligned and within every member's cached
+   tokens, members' first pages equal to the group's pages, seq_prefix_lens
+   consistent.  Any pointer may be NULL to skip its checks; launches nothing. */
+int mvr_paged_attention_cascade_validate(const mvr_paged_attention_args* args, const mvr_cascade_groups* groups,
+                                         const int32_t* block_tables_host, const int32_t* seq_lens_host,
+                                         const int32_t* cu_q_lens_host, const int32_t* group_cu_q_lens_host,
+                                         const int32_t* group_prefix_lens_host,
+                                         const int32_t* group_block_tables_host,
+                                         const int32_t* seq_prefix_lens_host);
+
 /* AttentionDimensions (common.rs:189-206). */
 typedef struct mvr_attention_dimensions {
   int32_t num_q_heads;

@@ -127,7 +127,7 @@ int device_cus() {
   return cus;
 }
 
-mvr::PagedAttentionPlan make_plan(const mvr_paged_attention_args* a) {
+mvr::PagedAttentionPlan make_plan(const mvr_paged_attention_args* a, bool allow_prefill = true) {
   mvr::PagedAttentionPlan plan{};
   plan.dtype = a->dtype;
   plan.head_dim = a->head_dim;
@@ -138,7 +138,7 @@ mvr::PagedAttentionPlan make_plan(const mvr_paged_attention_args* a) {
   // call on the split-context kernel.
   static const bool prefill_enabled = env_bool("MVR_ATTN_PREFILL_KERNEL", true);
   const bool page_pow2 = (a->page_size & (a->page_size - 1)) == 0;
-  if (prefill_enabled && a->dtype == MVR_DTYPE_F16 && rows_max > 64 && page_pow2) {
+  if (allow_prefill && prefill_enabled && a->dtype == MVR_DTYPE_F16 && rows_max > 64 && page_pow2) {
     plan.prefill = true;
     plan.row_tiles = (int)((rows_max + mvr::kPrefillBlockRows - 1) / mvr::kPrefillBlockRows);
     const int64_t base_blocks = (int64_t)a->num_seqs * a->num_kv_heads * plan.row_tiles;
@@ -150,8 +150,8 @@ mvr::PagedAttentionPlan make_plan(const mvr_paged_attention_args* a) {
       // per CU ran faster than two half-length blocks plus the merge pass.
       splits = (int64_t)device_cus() / base_blocks;
       if (splits > key_tiles / 8) splits = key_tiles / 8; // keep >= 8 key tiles per split
-      if (splits > 8) splits = 8;
     }
+    if (splits > 8) splits = 8; // the merge holds one split per lane; 8 is plenty
     if (splits < 1) splits = 1;
     plan.kv_splits = (int)splits;
     if (splits > 1) {
@@ -222,6 +222,174 @@ mvr::PagedAttentionPlan make_plan(const mvr_paged_attention_args* a) {
     plan.partial_bytes = align_up(prow * a->head_dim * sizeof(float), 256) + align_up(prow * 2 * sizeof(float), 256);
   }
   return plan;
+}
+
+} // namespace
+
+namespace {
+
+// The extra inputs of one pass of cascade attention (all null / 0 for a plain call).
+struct CascadePass {
+  const int32_t* key_begin = nullptr; // suffix pass: first key of each sequence
+  const int32_t* key_end = nullptr;   // prefix pass: keys [0, key_end) of each group
+  float* state_o = nullptr;           // normalised fp32 rows instead of `out`
+  float* state_lse = nullptr;
+  int32_t state_tokens = 0;
+};
+
+// Launches the planned kernel(s); workspace ws holds plan.partial_bytes.
+int launch_planned(const mvr_paged_attention_args* a, const mvr::PagedAttentionPlan& plan, void* ws,
+                   const CascadePass& cp) {
+  const float scale = a->scale > 0.f ? a->scale : (float)(1.0 / sqrt((double)a->head_dim));
+  if (plan.prefill) {
+    mvr::PrefillParams f{};
+    f.q = a->q;
+    f.q_stride_head = a->q_stride_head;
+    f.q_stride_token = a->q_stride_token;
+    f.key_pool = a->key_pool;
+    f.value_pool = a->value_pool;
+    f.block_tables = a->block_tables;
+    f.block_table_stride = a->max_pages_per_seq;
+    f.seq_lens = a->seq_lens;
+    f.cu_q_lens = a->cu_q_lens;
+    f.single_seq_len = a->max_seq_len;
+    f.single_q_len = a->max_q_len;
+    f.out = a->out;
+    f.out_stride_head = a->out_stride_head;
+    f.out_stride_token = a->out_stride_token;
+    if (plan.partial_bytes) {
+      const size_t prow = (size_t)a->num_seqs * a->num_kv_heads * plan.row_tiles * plan.kv_splits *
+                          mvr::kPrefillBlockRows;
+      char* w = static_cast<char*>(ws);
+      f.partial_o = reinterpret_cast<float*>(w);
+      f.partial_ml = reinterpret_cast<float*>(w + align_up(prow * a->head_dim * sizeof(float), 256));
+    }
+    f.num_seqs = a->num_seqs;
+    f.num_kv_heads = a->num_kv_heads;
+    f.group_size = a->num_q_heads / a->num_kv_heads;
+    f.page_size = a->page_size;
+    f.page_shift = 0;
+    while ((1 << f.page_shift) < a->page_size) f.page_shift++; // page_size is a power of two here
+    f.row_tiles = plan.row_tiles;
+    f.kv_splits = plan.kv_splits;
+    f.scale_log2 = scale * 1.4426950408889634f;
+    f.key_end = cp.key_end;
+    f.state_o = cp.state_o;
+    f.state_lse = cp.state_lse;
+    f.state_tokens = cp.state_tokens;
+    TraceRange launch("attn-prefill-fused");
+    hipError_t err = mvr::launch_paged_prefill(f, a->head_dim, static_cast<hipStream_t>(a->stream));
+    if (err != hipSuccess) return fail(MVR_E_HIP, "kernel launch failed: %s", hipGetErrorString(err));
+    return MVR_OK;
+  }
+
+  mvr::PagedAttentionParams p{};
+  p.q = a->q;
+  p.q_stride_head = a->q_stride_head;
+  p.q_stride_token = a->q_stride_token;
+  p.key_pool = a->key_pool;
+  p.value_pool = a->value_pool;
+  p.block_tables = a->block_tables;
+  p.block_table_stride = a->max_pages_per_seq;
+  p.seq_lens = a->seq_lens;
+  p.cu_q_lens = a->cu_q_lens;
+  p.single_seq_len = a->max_seq_len;
+  p.single_q_len = a->max_q_len;
+  p.out = a->out;
+  p.out_stride_head = a->out_stride_head;
+  p.out_stride_token = a->out_stride_token;
+  if (plan.partial_bytes) {
+    const size_t prow = (size_t)plan.num_units * 16 * plan.row_blocks;
+    char* w = static_cast<char*>(ws);
+    p.partial_o = reinterpret_cast<float*>(w);
+    p.partial_ml = reinterpret_cast<float*>(w + align_up(prow * a->head_dim * sizeof(float), 256));
+  }
+  p.num_seqs = a->num_seqs;
+  p.num_kv_heads = a->num_kv_heads;
+  p.group_size = a->num_q_heads / a->num_kv_heads;
+  p.page_size = a->page_size;
+  p.scale_log2 = scale * 1.4426950408889634f;
+  p.key_begin = cp.key_begin;
+  p.key_end = cp.key_end;
+  p.state_o = cp.state_o;
+  p.state_lse = cp.state_lse;
+  p.state_tokens = cp.state_tokens;
+
+  TraceRange launch("attn-paged-fused"); // one launch replaces attn-qk / attn-mask-softmax / attn-paged-v
+  hipError_t err = mvr::launch_paged_attention(plan, p, static_cast<hipStream_t>(a->stream));
+  if (err != hipSuccess) return fail(MVR_E_HIP, "kernel launch failed: %s", hipGetErrorString(err));
+  return MVR_OK;
+}
+
+int check_workspace(const mvr_paged_attention_args* a, size_t need) {
+  if (a->workspace_bytes < need || (need && !a->workspace))
+    return fail(MVR_E_WORKSPACE, "workspace of %zu bytes is smaller than the %zu bytes required", a->workspace_bytes,
+                need);
+  if (need && ((uintptr_t)a->workspace & 255u)) return fail(MVR_E_INVALID_ARGUMENT, "workspace must be 256-byte aligned");
+  return MVR_OK;
+}
+
+// Cascade attention: a prefix pass over the groups' shared pages (each
+// group's members' query rows as one virtual sequence whose keys end at the
+// prefix), a suffix pass per sequence from its prefix on, and a merge of the
+// two normalised states.  Workspace: [prefix partials][suffix partials]
+// [state A o][state A lse][state B o][state B lse].
+struct CascadePlan {
+  mvr_paged_attention_args pre, suf;
+  mvr::PagedAttentionPlan pre_plan, suf_plan;
+  int32_t state_tokens; // bound of the packed token count: state row stride
+  size_t off_suf, off_a_o, off_a_lse, off_b_o, off_b_lse, total;
+};
+
+int check_cascade(const mvr_paged_attention_args* a, const mvr_cascade_groups* g) {
+  int rc = check_scalars(a);
+  if (rc != MVR_OK) return rc;
+  if (!g) return fail(MVR_E_INVALID_ARGUMENT, "groups is null");
+  if (g->num_groups < 0 || g->num_groups > a->num_seqs)
+    return fail(MVR_E_INVALID_ARGUMENT, "num_groups %d is outside [0, num_seqs]", g->num_groups);
+  if (!g->seq_prefix_lens) return fail(MVR_E_INVALID_ARGUMENT, "seq_prefix_lens is required");
+  if (g->num_groups > 0) {
+    if (!g->group_cu_q_lens || !g->group_prefix_lens || !g->group_block_tables)
+      return fail(MVR_E_INVALID_ARGUMENT, "group tables are required when num_groups > 0");
+    if (g->max_group_q_len < 1 || g->max_prefix_len < 0)
+      return fail(MVR_E_INVALID_ARGUMENT, "max_group_q_len must be positive and max_prefix_len non-negative");
+    if (g->max_prefix_len > a->max_seq_len)
+      return fail(MVR_E_INVALID_ARGUMENT, "max_prefix_len %d exceeds max_seq_len %d", g->max_prefix_len, a->max_seq_len);
+    if ((int64_t)g->max_group_q_len > (int64_t)a->num_seqs * a->max_q_len)
+      return fail(MVR_E_INVALID_ARGUMENT, "max_group_q_len %d exceeds the packed token bound", g->max_group_q_len);
+  }
+  if (g->sum_prefix_lens < 0 || (a->sum_seq_lens > 0 && g->sum_prefix_lens > a->sum_seq_lens))
+    return fail(MVR_E_INVALID_ARGUMENT, "sum_prefix_lens %lld is outside [0, sum_seq_lens]", (long long)g->sum_prefix_lens);
+  return MVR_OK;
+}
+
+CascadePlan make_cascade_plan(const mvr_paged_attention_args* a, const mvr_cascade_groups* g) {
+  CascadePlan c;
+  c.state_tokens = a->num_seqs * a->max_q_len;
+  c.pre = *a;
+  c.pre.num_seqs = g->num_groups > 0 ? g->num_groups : 1;
+  c.pre.cu_q_lens = g->group_cu_q_lens;
+  c.pre.seq_lens = nullptr; // the prefix pass derives each group's limits from its prefix length
+  c.pre.block_tables = g->group_block_tables;
+  c.pre.max_q_len = g->num_groups > 0 ? g->max_group_q_len : 1;
+  c.pre.max_seq_len = (g->num_groups > 0 ? g->max_prefix_len : 1) + c.pre.max_q_len;
+  c.pre.sum_seq_lens = 0;
+  c.pre_plan = g->num_groups > 0 ? make_plan(&c.pre) : mvr::PagedAttentionPlan{};
+  c.suf = *a;
+  c.suf.sum_seq_lens =
+      a->sum_seq_lens > 0 && g->sum_prefix_lens > 0 ? a->sum_seq_lens - g->sum_prefix_lens : a->sum_seq_lens;
+  if (c.suf.sum_seq_lens >= (int64_t)a->max_seq_len * a->num_seqs) c.suf.sum_seq_lens = 0;
+  // The suffix pass starts every sequence at its prefix: split-context kernel.
+  c.suf_plan = make_plan(&c.suf, /*allow_prefill=*/false);
+  const size_t so = (size_t)a->num_q_heads * c.state_tokens * a->head_dim * sizeof(float);
+  const size_t sl = (size_t)a->num_q_heads * c.state_tokens * sizeof(float);
+  c.off_suf = align_up(c.pre_plan.partial_bytes, 256);
+  c.off_a_o = c.off_suf + align_up(c.suf_plan.partial_bytes, 256);
+  c.off_a_lse = c.off_a_o + align_up(so, 256);
+  c.off_b_o = c.off_a_lse + align_up(sl, 256);
+  c.off_b_lse = c.off_b_o + align_up(so, 256);
+  c.total = c.off_b_lse + align_up(sl, 256);
+  return c;
 }
 
 } // namespace
@@ -387,81 +555,113 @@ int mvr_paged_attention(const mvr_paged_attention_args* a) {
   int rc = check_scalars(a);
   if (rc != MVR_OK) return rc;
   const mvr::PagedAttentionPlan plan = make_plan(a);
-  if (a->workspace_bytes < plan.partial_bytes || (plan.partial_bytes && !a->workspace))
-    return fail(MVR_E_WORKSPACE, "workspace of %zu bytes is smaller than the %zu bytes required", a->workspace_bytes,
-                plan.partial_bytes);
-  if (plan.partial_bytes && ((uintptr_t)a->workspace & 255u))
-    return fail(MVR_E_INVALID_ARGUMENT, "workspace must be 256-byte aligned");
-  const float scale = a->scale > 0.f ? a->scale : (float)(1.0 / sqrt((double)a->head_dim));
+  rc = check_workspace(a, plan.partial_bytes);
+  if (rc != MVR_OK) return rc;
+  return launch_planned(a, plan, a->workspace, CascadePass());
+}
 
-  if (plan.prefill) {
-    mvr::PrefillParams f{};
-    f.q = a->q;
-    f.q_stride_head = a->q_stride_head;
-    f.q_stride_token = a->q_stride_token;
-    f.key_pool = a->key_pool;
-    f.value_pool = a->value_pool;
-    f.block_tables = a->block_tables;
-    f.block_table_stride = a->max_pages_per_seq;
-    f.seq_lens = a->seq_lens;
-    f.cu_q_lens = a->cu_q_lens;
-    f.single_seq_len = a->max_seq_len;
-    f.single_q_len = a->max_q_len;
-    f.out = a->out;
-    f.out_stride_head = a->out_stride_head;
-    f.out_stride_token = a->out_stride_token;
-    if (plan.partial_bytes) {
-      const size_t prow = (size_t)a->num_seqs * a->num_kv_heads * plan.row_tiles * plan.kv_splits *
-                          mvr::kPrefillBlockRows;
-      char* ws = static_cast<char*>(a->workspace);
-      f.partial_o = reinterpret_cast<float*>(ws);
-      f.partial_ml = reinterpret_cast<float*>(ws + align_up(prow * a->head_dim * sizeof(float), 256));
-    }
-    f.num_seqs = a->num_seqs;
-    f.num_kv_heads = a->num_kv_heads;
-    f.group_size = a->num_q_heads / a->num_kv_heads;
-    f.page_size = a->page_size;
-    f.page_shift = 0;
-    while ((1 << f.page_shift) < a->page_size) f.page_shift++; // page_size is a power of two here
-    f.row_tiles = plan.row_tiles;
-    f.kv_splits = plan.kv_splits;
-    f.scale_log2 = scale * 1.4426950408889634f;
-    TraceRange launch("attn-prefill-fused");
-    hipError_t err = mvr::launch_paged_prefill(f, a->head_dim, static_cast<hipStream_t>(a->stream));
-    if (err != hipSuccess) return fail(MVR_E_HIP, "kernel launch failed: %s", hipGetErrorString(err));
-    return MVR_OK;
+size_t mvr_paged_attention_cascade_workspace_size(const mvr_paged_attention_args* args,
+                                                  const mvr_cascade_groups* groups) {
+  if (check_cascade(args, groups) != MVR_OK) return 0;
+  return make_cascade_plan(args, groups).total;
+}
+
+int mvr_paged_attention_cascade(const mvr_paged_attention_args* a, const mvr_cascade_groups* g) {
+  TraceRange range("attn");
+  g_last_error[0] = 0;
+  int rc = check_cascade(a, g);
+  if (rc != MVR_OK) return rc;
+  const CascadePlan c = make_cascade_plan(a, g);
+  rc = check_workspace(a, c.total);
+  if (rc != MVR_OK) return rc;
+  char* ws = static_cast<char*>(a->workspace);
+  float* a_o = reinterpret_cast<float*>(ws + c.off_a_o);
+  float* a_lse = reinterpret_cast<float*>(ws + c.off_a_lse);
+  float* b_o = reinterpret_cast<float*>(ws + c.off_b_o);
+  float* b_lse = reinterpret_cast<float*>(ws + c.off_b_lse);
+  if (g->num_groups > 0) {
+    CascadePass pre;
+    pre.key_end = g->group_prefix_lens;
+    pre.state_o = a_o;
+    pre.state_lse = a_lse;
+    pre.state_tokens = c.state_tokens;
+    rc = launch_planned(&c.pre, c.pre_plan, ws, pre);
+    if (rc != MVR_OK) return rc;
   }
-
+  CascadePass suf;
+  suf.key_begin = g->seq_prefix_lens;
+  suf.state_o = b_o;
+  suf.state_lse = b_lse;
+  suf.state_tokens = c.state_tokens;
+  rc = launch_planned(&c.suf, c.suf_plan, ws + c.off_suf, suf);
+  if (rc != MVR_OK) return rc;
   mvr::PagedAttentionParams p{};
-  p.q = a->q;
-  p.q_stride_head = a->q_stride_head;
-  p.q_stride_token = a->q_stride_token;
-  p.key_pool = a->key_pool;
-  p.value_pool = a->value_pool;
-  p.block_tables = a->block_tables;
-  p.block_table_stride = a->max_pages_per_seq;
-  p.seq_lens = a->seq_lens;
   p.cu_q_lens = a->cu_q_lens;
-  p.single_seq_len = a->max_seq_len;
   p.single_q_len = a->max_q_len;
-  p.out = a->out;
-  p.out_stride_head = a->out_stride_head;
-  p.out_stride_token = a->out_stride_token;
-  if (plan.partial_bytes) {
-    const size_t prow = (size_t)plan.num_units * 16 * plan.row_blocks;
-    char* ws = static_cast<char*>(a->workspace);
-    p.partial_o = reinterpret_cast<float*>(ws);
-    p.partial_ml = reinterpret_cast<float*>(ws + align_up(prow * a->head_dim * sizeof(float), 256));
-  }
   p.num_seqs = a->num_seqs;
   p.num_kv_heads = a->num_kv_heads;
   p.group_size = a->num_q_heads / a->num_kv_heads;
-  p.page_size = a->page_size;
-  p.scale_log2 = scale * 1.4426950408889634f;
-
-  TraceRange launch("attn-paged-fused"); // one launch replaces attn-qk / attn-mask-softmax / attn-paged-v
-  hipError_t err = mvr::launch_paged_attention(plan, p, static_cast<hipStream_t>(a->stream));
+  p.out = a->out;
+  p.out_stride_head = a->out_stride_head;
+  p.out_stride_token = a->out_stride_token;
+  p.state_o = b_o;
+  p.state_lse = b_lse;
+  p.state_tokens = c.state_tokens;
+  hipError_t err = mvr::launch_merge_states(p, a->dtype, a->head_dim, a_o, a_lse, g->seq_prefix_lens, c.state_tokens,
+                                            static_cast<hipStream_t>(a->stream));
   if (err != hipSuccess) return fail(MVR_E_HIP, "kernel launch failed: %s", hipGetErrorString(err));
+  return MVR_OK;
+}
+
+int mvr_paged_attention_cascade_validate(const mvr_paged_attention_args* a, const mvr_cascade_groups* g,
+                                         const int32_t* bt, const int32_t* seq_lens, const int32_t* cu,
+                                         const int32_t* gcu, const int32_t* gpre, const int32_t* gbt,
+                                         const int32_t* spre) {
+  g_last_error[0] = 0;
+  int rc = check_cascade(a, g);
+  if (rc != MVR_OK) return rc;
+  rc = mvr_paged_attention_validate(a, bt, seq_lens, cu);
+  if (rc != MVR_OK) return rc;
+  if (!gcu || !cu) return MVR_OK;
+  const int ng = g->num_groups;
+  int s = 0; // sequences before the current group must carry no prefix
+  for (int gi = 0; gi < ng; gi++) {
+    if (gcu[gi + 1] <= gcu[gi])
+      return fail(MVR_E_INVALID_ARGUMENT, "group %d has no query tokens", gi);
+    if (gcu[gi + 1] - gcu[gi] > g->max_group_q_len)
+      return fail(MVR_E_INVALID_ARGUMENT, "group %d has %d query tokens > max_group_q_len %d", gi,
+                  gcu[gi + 1] - gcu[gi], g->max_group_q_len);
+    // Members: the consecutive sequences whose tokens span [gcu[gi], gcu[gi+1]).
+    while (s < a->num_seqs && cu[s] < gcu[gi]) {
+      if (spre && spre[s] != 0)
+        return fail(MVR_E_INVALID_ARGUMENT, "sequence %d is in no group but has seq_prefix_lens %d", s, spre[s]);
+      s++;
+    }
+    if (s >= a->num_seqs || cu[s] != gcu[gi])
+      return fail(MVR_E_INVALID_ARGUMENT, "group %d does not start at a sequence boundary", gi);
+    const int pre = gpre ? gpre[gi] : -1;
+    if (gpre && (pre < 0 || pre % a->page_size || pre > g->max_prefix_len))
+      return fail(MVR_E_INVALID_ARGUMENT, "group %d prefix %d is not a multiple of page_size %d within max_prefix_len",
+                  gi, pre, a->page_size);
+    for (; s < a->num_seqs && cu[s] < gcu[gi + 1]; s++) {
+      if (cu[s + 1] > gcu[gi + 1])
+        return fail(MVR_E_INVALID_ARGUMENT, "group %d does not end at a sequence boundary", gi);
+      if (spre && gpre && spre[s] != pre)
+        return fail(MVR_E_INVALID_ARGUMENT, "sequence %d has seq_prefix_lens %d, its group's prefix is %d", s, spre[s], pre);
+      if (gpre && seq_lens) {
+        const int cached = seq_lens[s] - (cu[s + 1] - cu[s]);
+        if (pre > cached)
+          return fail(MVR_E_INVALID_ARGUMENT, "group %d prefix %d exceeds sequence %d's %d cached tokens", gi, pre, s, cached);
+      }
+      if (gpre && bt && gbt)
+        for (int pi = 0; pi < pre / a->page_size; pi++)
+          if (bt[(int64_t)s * a->max_pages_per_seq + pi] != gbt[(int64_t)gi * a->max_pages_per_seq + pi])
+            return fail(MVR_E_INVALID_ARGUMENT, "sequence %d page %d differs from its group's shared page", s, pi);
+    }
+  }
+  for (; s < a->num_seqs; s++)
+    if (spre && spre[s] != 0)
+      return fail(MVR_E_INVALID_ARGUMENT, "sequence %d is in no group but has seq_prefix_lens %d", s, spre[s]);
   return MVR_OK;
 }
 

@@ -53,8 +53,11 @@ __device__ __forceinline__ float wave_sum_across_groups(float v) {
 }
 
 // Per-sequence metadata (seq_lens / cu_q_lens may be absent for one request).
+// Keys [key_begin, key_end) are this call's share of the context: all of it
+// normally; the suffix after a shared prefix, or the prefix itself (where
+// every row sees every prefix key), in the two passes of cascade attention.
 struct SeqInfo {
-  int seq_len, q_start, q_len;
+  int seq_len, q_start, q_len, key_begin, key_end;
 };
 
 __device__ __forceinline__ SeqInfo load_seq(const PagedAttentionParams& p, int b) {
@@ -67,20 +70,36 @@ __device__ __forceinline__ SeqInfo load_seq(const PagedAttentionParams& p, int b
     s.q_start = 0;
     s.q_len = p.single_q_len;
   }
+  s.key_begin = p.key_begin ? p.key_begin[b] : 0;
+  if (p.key_end) {
+    s.key_end = p.key_end[b];
+    s.seq_len = s.key_end + s.q_len; // every row's causal limit reaches past the prefix
+  } else {
+    s.key_end = s.seq_len;
+  }
   return s;
 }
 
+// Causal limit of query i: key j visible iff j <= seq_len - q_len + i
+// (common.rs:948-965), within this call's keys.
+__device__ __forceinline__ int row_limit(const SeqInfo& s, int i) { return min(s.seq_len - s.q_len + i, s.key_end - 1); }
+
 // Number of 16-token chunks row tile rt of a sequence must visit: keys up to
-// the largest causal limit among its rows (key j visible to query i iff
-// j <= seq_len - q_len + i, common.rs:948-965).
+// the largest causal limit among its rows.
 __device__ __forceinline__ int tile_chunks(const SeqInfo& s, int group_size, int rt, int tile_rows) {
   const int rows = group_size * s.q_len;
   const int rho0 = rt * tile_rows;
   if (rho0 >= rows || s.q_len <= 0) return 0;
   const int rho1 = min(rho0 + tile_rows, rows) - 1;
   const int max_i = (rho1 / s.q_len != rho0 / s.q_len) ? s.q_len - 1 : rho1 % s.q_len;
-  const int last_key = s.seq_len - s.q_len + max_i;
-  return last_key / kChunkTokens + 1;
+  const int last_key = row_limit(s, max_i); // -1: no key (a prefix pass over an empty prefix)
+  return last_key < 0 ? 0 : last_key / kChunkTokens + 1;
+}
+
+// Partitions of a row tile: chunks [key_begin/16, n_chunks) in chunks_per_part pieces.
+__device__ __forceinline__ int tile_parts(const SeqInfo& s, int n_chunks, int chunks_per_part) {
+  const int kb = s.key_begin / kChunkTokens;
+  return n_chunks > kb ? (n_chunks - kb + chunks_per_part - 1) / chunks_per_part : 0;
 }
 
 // ---------------------------------------------------------------------------
@@ -278,10 +297,10 @@ __global__ __launch_bounds__(kWaveSize* kWavesPerBlock, Tr::template min_blocks<
   const SeqInfo s = load_seq(p, b);
   const int rows = p.group_size * s.q_len;
   const int n_chunks = tile_chunks(s, p.group_size, rt, kTileRows);
-  const int k0 = part * p.chunks_per_part;
+  const int k0 = s.key_begin / kChunkTokens + part * p.chunks_per_part;
   if (n_chunks == 0 || k0 >= n_chunks) return;
   const int k1 = min(k0 + p.chunks_per_part, n_chunks);
-  const int n_parts = (n_chunks + p.chunks_per_part - 1) / p.chunks_per_part;
+  const int n_parts = tile_parts(s, n_chunks, p.chunks_per_part);
   const int g = l >> 4;
 
   // Query rows of this lane (one per row block) and their causal limits.
@@ -297,7 +316,7 @@ __global__ __launch_bounds__(kWaveSize* kWavesPerBlock, Tr::template min_blocks<
     const int i = row_valid[nb] ? rho % s.q_len : 0;
     q_head[nb] = h * p.group_size + r;
     q_tok[nb] = s.q_start + i;
-    limit[nb] = row_valid[nb] ? s.seq_len - s.q_len + i : s.seq_len - 1;
+    limit[nb] = row_valid[nb] ? row_limit(s, i) : s.key_end - 1;
     const T* qrow = static_cast<const T*>(p.q) + (int64_t)q_head[nb] * p.q_stride_head + (int64_t)q_tok[nb] * p.q_stride_token;
     Tr::load_q(qrow, row_valid[nb], g, q[nb]);
   }
@@ -329,7 +348,7 @@ __global__ __launch_bounds__(kWaveSize* kWavesPerBlock, Tr::template min_blocks<
   auto process = [&](int k, const typename Tr::kreg_t (&kr)[Tr::kLoads], const typename Tr::vreg_t (&vr)[Tr::kLoads]) {
     const int tok0 = k * kChunkTokens;
     asm volatile("" ::: "memory");
-    Tr::stage_v(lds, l, s.seq_len - tok0, vr);
+    Tr::stage_v(lds, l, s.key_end - tok0, vr);
     float pr[NB][4];
 #pragma unroll
     for (int nb = 0; nb < NB; nb++) {
@@ -388,9 +407,18 @@ __global__ __launch_bounds__(kWaveSize* kWavesPerBlock, Tr::template min_blocks<
     if (n_parts == 1) {
       if (row_valid[nb]) {
         const float inv = 1.f / ltot;
-        T* dst = static_cast<T*>(p.out) + (int64_t)q_head[nb] * p.out_stride_head + (int64_t)q_tok[nb] * p.out_stride_token;
+        if (p.state_o) {
+          const int64_t srow = (int64_t)q_head[nb] * p.state_tokens + q_tok[nb];
+          float* dst = p.state_o + srow * D;
 #pragma unroll
-        for (int n = 0; n < D / 16; n++) Tr::store_out(dst + 16 * n + 4 * g, o[nb][n] * inv);
+          for (int n = 0; n < D / 16; n++) *reinterpret_cast<float4v*>(dst + 16 * n + 4 * g) = o[nb][n] * inv;
+          if (g == 0) p.state_lse[srow] = m[nb] + __log2f(ltot);
+        } else {
+          T* dst =
+              static_cast<T*>(p.out) + (int64_t)q_head[nb] * p.out_stride_head + (int64_t)q_tok[nb] * p.out_stride_token;
+#pragma unroll
+          for (int n = 0; n < D / 16; n++) Tr::store_out(dst + 16 * n + 4 * g, o[nb][n] * inv);
+        }
       }
     } else {
       const int64_t prow = slot * kTileRows + nb * 16 + (l & 15);
@@ -433,7 +461,7 @@ __global__ __launch_bounds__(256) void merge_partitions_kernel(PagedAttentionPar
   const int rho = rt * kTileRows + lr;
   if (rho >= p.group_size * s.q_len) return;
   const int n_chunks = tile_chunks(s, p.group_size, rt, kTileRows);
-  const int n_parts = (n_chunks + p.chunks_per_part - 1) / p.chunks_per_part;
+  const int n_parts = tile_parts(s, n_chunks, p.chunks_per_part);
   if (n_parts <= 1) return;
 
   // Partial row of partition j: (tile * max_parts + j) * kTileRows + lr.
@@ -480,11 +508,67 @@ __global__ __launch_bounds__(256) void merge_partitions_kernel(PagedAttentionPar
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) den += __shfl_xor(den, off);
   const int r = rho / s.q_len, i = rho % s.q_len;
+  const float inv = 1.f / den;
+  if (p.state_o) {
+    const int64_t srow = (int64_t)(h * p.group_size + r) * p.state_tokens + s.q_start + i;
+#pragma unroll
+    for (int e = 0; e < kPer; e++) p.state_o[srow * D + l * kPer + e] = acc[e] * inv;
+    if (l == 0) p.state_lse[srow] = m_use + __log2f(den);
+    return;
+  }
   T* dst = static_cast<T*>(p.out) + (int64_t)(h * p.group_size + r) * p.out_stride_head +
            (int64_t)(s.q_start + i) * p.out_stride_token + l * kPer;
-  const float inv = 1.f / den;
 #pragma unroll
   for (int e = 0; e < kPer; e++) dst[e] = (T)(acc[e] * inv);
+}
+
+// Cascade merge of two attention states per output row (q head, packed
+// token): A from the shared-prefix pass (sequences in a prefix group only),
+// B from the suffix pass; out = (2^(lse_a - M) o_a + 2^(lse_b - M) o_b) /
+// (2^(lse_a - M) + 2^(lse_b - M)).  One wavefront per row; total_q bounds
+// the packed token count (rows past cu_q_lens[num_seqs] exit).
+template <typename T, int D>
+__global__ __launch_bounds__(256) void merge_states_kernel(PagedAttentionParams p, const float* a_o,
+                                                           const float* a_lse, const int32_t* seq_prefix_len,
+                                                           int32_t total_q) {
+  constexpr int kPer = D / kWaveSize;
+  const int64_t row = (int64_t)blockIdx.x * kWavesPerBlock + __builtin_amdgcn_readfirstlane(threadIdx.x / kWaveSize);
+  const int hq = p.num_kv_heads * p.group_size;
+  const int qh = (int)(row / total_q);
+  const int n = (int)(row - (int64_t)qh * total_q);
+  if (qh >= hq) return;
+  // total_q is a host-side bound; tokens past the real packed count exit.
+  const const_i32* cu = (const const_i32*)p.cu_q_lens;
+  if (n >= (p.cu_q_lens ? cu[p.num_seqs] : p.single_q_len)) return;
+  int b = 0;
+  if (p.cu_q_lens) { // largest b with cu_q_lens[b] <= n: uniform, scalar loads
+    int lo = 0, hi = p.num_seqs - 1;
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (cu[mid] <= n)
+        lo = mid;
+      else
+        hi = mid - 1;
+    }
+    b = lo;
+  }
+  const bool has_prefix = ((const const_i32*)seq_prefix_len)[b] > 0;
+  const int l = lane_id();
+  const int64_t srow = (int64_t)qh * p.state_tokens + n;
+  float out[kPer];
+#pragma unroll
+  for (int e = 0; e < kPer; e++) out[e] = p.state_o[srow * D + l * kPer + e];
+  if (has_prefix) {
+    const float la = a_lse[srow], lb = p.state_lse[srow];
+    const float mx = fmaxf(la, lb);
+    const float wa = exp2f(la - mx), wb = exp2f(lb - mx);
+    const float inv = 1.f / (wa + wb);
+#pragma unroll
+    for (int e = 0; e < kPer; e++) out[e] = (wa * a_o[srow * D + l * kPer + e] + wb * out[e]) * inv;
+  }
+  T* dst = static_cast<T*>(p.out) + (int64_t)qh * p.out_stride_head + (int64_t)n * p.out_stride_token + l * kPer;
+#pragma unroll
+  for (int e = 0; e < kPer; e++) dst[e] = (T)out[e];
 }
 
 template <typename Tr, int D, int NB>
@@ -521,6 +605,28 @@ hipError_t launch_paged_attention(const PagedAttentionPlan& plan, PagedAttention
     MVR_DISPATCH(F32Traits, 128, 2)
   }
 #undef MVR_DISPATCH
+  return hipErrorInvalidValue;
+}
+
+hipError_t launch_merge_states(const PagedAttentionParams& p, int dtype, int head_dim, const float* prefix_o,
+                               const float* prefix_lse, const int32_t* seq_prefix_len, int32_t total_q,
+                               hipStream_t stream) {
+  const int64_t rows = (int64_t)p.num_kv_heads * p.group_size * total_q;
+  const dim3 grid((unsigned)((rows + kWavesPerBlock - 1) / kWavesPerBlock)), block(kWaveSize * kWavesPerBlock);
+#define MVR_MERGE(T, DD)                                                                                        \
+  if (head_dim == DD) {                                                                                         \
+    hipLaunchKernelGGL((merge_states_kernel<T, DD>), grid, block, 0, stream, p, prefix_o, prefix_lse, seq_prefix_len, \
+                       total_q);                                                                                \
+    return hipGetLastError();                                                                                   \
+  }
+  if (dtype == 1) {
+    MVR_MERGE(half_t, 64)
+    MVR_MERGE(half_t, 128)
+  } else {
+    MVR_MERGE(float, 64)
+    MVR_MERGE(float, 128)
+  }
+#undef MVR_MERGE
   return hipErrorInvalidValue;
 }
 

@@ -37,6 +37,12 @@ struct PagedAttentionParams {
   int32_t row_tiles;       // row tiles per (sequence, kv head)
   int64_t num_units;
   float scale_log2; // softmax scale * log2(e)
+  // Cascade passes (all optional, null / 0 otherwise):
+  const int32_t* key_begin; // per sequence: first key (a multiple of 16); earlier keys belong to the prefix pass
+  const int32_t* key_end;   // per sequence: prefix pass, keys [0, key_end), every query row sees all of them
+  float* state_o;           // write normalised fp32 rows [q head][state_tokens][D] instead of `out` ...
+  float* state_lse;         // ... and their log2-sum-exp [q head][state_tokens]
+  int32_t state_tokens;
 };
 
 // Grid shape chosen by the host.
@@ -54,6 +60,14 @@ struct PagedAttentionPlan {
 };
 
 hipError_t launch_paged_attention(const PagedAttentionPlan& plan, PagedAttentionParams params, hipStream_t stream);
+
+// Cascade merge: out[q head][token] from the prefix-pass state (prefix_o,
+// prefix_lse; used where seq_prefix_len of the token's sequence is > 0) and
+// the suffix-pass state in params.state_o / state_lse; total_q bounds the
+// packed token count.
+hipError_t launch_merge_states(const PagedAttentionParams& params, int dtype, int head_dim, const float* prefix_o,
+                               const float* prefix_lse, const int32_t* seq_prefix_len, int32_t total_q,
+                               hipStream_t stream);
 
 // Wavefronts of the plan's kernel variant the current device holds at once
 // (occupancy x waves per block x CUs); 0 if the device cannot be queried.

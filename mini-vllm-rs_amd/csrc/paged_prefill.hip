@@ -54,7 +54,7 @@ constexpr int kStages = MVR_PREFILL_STAGES; // LDS stages (4 or 8): the unrolled
 constexpr float kRescaleThreshold = 8.0f; // log2 units: p <= 2^8 between rescales
 
 struct SeqRows {
-  int seq_len, q_start, q_len;
+  int seq_len, q_start, q_len, key_end; // keys [0, key_end) belong to this call
 };
 
 // Tile barrier: waits until at most kNewer of this wavefront's direct-to-LDS
@@ -89,8 +89,17 @@ __device__ __forceinline__ SeqRows load_rows(const PrefillParams& p, int b) {
     s.q_start = 0;
     s.q_len = p.single_q_len;
   }
+  if (p.key_end) { // cascade prefix pass: every row sees every key before key_end
+    s.key_end = p.key_end[b];
+    s.seq_len = s.key_end + s.q_len;
+  } else {
+    s.key_end = s.seq_len;
+  }
   return s;
 }
+
+// Causal limit of query i within this call's keys (common.rs:948-965).
+__device__ __forceinline__ int row_limit(const SeqRows& s, int i) { return min(s.seq_len - s.q_len + i, s.key_end - 1); }
 
 // Keys the block's rows can see: up to the largest causal limit among them.
 __device__ __forceinline__ int block_key_tiles(const SeqRows& s, int group_size, int rt) {
@@ -99,8 +108,8 @@ __device__ __forceinline__ int block_key_tiles(const SeqRows& s, int group_size,
   if (rho0 >= rows || s.q_len <= 0) return 0;
   const int rho1 = min(rho0 + kBlockRows, rows) - 1;
   const int max_i = (rho1 / s.q_len != rho0 / s.q_len) ? s.q_len - 1 : rho1 % s.q_len;
-  const int last_key = s.seq_len - s.q_len + max_i;
-  return last_key / kTileTokens + 1;
+  const int last_key = row_limit(s, max_i); // -1: no key (a prefix pass over an empty prefix)
+  return last_key < 0 ? 0 : last_key / kTileTokens + 1;
 }
 
 template <int D>
@@ -170,7 +179,7 @@ __global__ __launch_bounds__(kWaves * 64, D == 128 ? 1 : 2) void paged_prefill_k
   const bool valid = rho < rows;
   const int r = valid ? rho / s.q_len : 0;
   const int i = valid ? rho % s.q_len : 0;
-  const int limit = valid ? s.seq_len - s.q_len + i : -1;
+  const int limit = valid ? row_limit(s, i) : -1;
   // Largest causal limit among the wave's rows (rows of a wave are contiguous).
   int wave_limit = limit;
   for (int off = 1; off < 64; off <<= 1) wave_limit = max(wave_limit, __shfl_xor(wave_limit, off));
@@ -224,7 +233,7 @@ __global__ __launch_bounds__(kWaves * 64, D == 128 ? 1 : 2) void paged_prefill_k
     ld_k[u] = 8 * (cs ^ TL::kswz(t));
     ld_v[u] = 8 * (2 * ((cs >> 1) ^ TL::vswz(t)) + (cs & 1));
   }
-  // Branch-free: tokens past the sequence end re-read the last valid token,
+  // Branch-free: tokens past the call's last key re-read that key,
   // so every tile issues the same loads.  Those duplicate keys lie past every
   // row's causal limit (the last tile is a diagonal tile for every wavefront
   // that sees it), so their scores are masked to -inf, p = 0, and
@@ -240,13 +249,13 @@ __global__ __launch_bounds__(kWaves * 64, D == 128 ? 1 : 2) void paged_prefill_k
     Pages r;
 #pragma unroll
     for (int u = 0; u < TL::kChunksPerThread; u++)
-      r.pg[u] = bt[page_div(min(j * kTileTokens + ld_t0[u], s.seq_len - 1))]; // wave-uniform: scalar load
+      r.pg[u] = bt[page_div(min(j * kTileTokens + ld_t0[u], s.key_end - 1))]; // wave-uniform: scalar load
     return r;
   };
   auto issue_tile = [&](int j, const Pages& pages, half_t* kb, half_t* vb) {
 #pragma unroll
     for (int u = 0; u < TL::kChunksPerThread; u++) {
-      const int tg = min(j * kTileTokens + ld_t[u], s.seq_len - 1);
+      const int tg = min(j * kTileTokens + ld_t[u], s.key_end - 1);
       const int64_t row = ((pages.pg[u] * p.num_kv_heads + h) * p.page_size + page_mod(tg)) * D;
       const int dst = (u * kWaves + wave) * 64 * 8;
       load_to_lds16(kpool + row + ld_k[u], kb + dst);
@@ -431,7 +440,7 @@ __global__ __launch_bounds__(kWaves * 64, D == 128 ? 1 : 2) void paged_prefill_k
     const int rho0 = rt * kBlockRows;
     const int rho_last = min(rho0 + kBlockRows, rows) - 1;
     const int min_i = rho0 / s.q_len != rho_last / s.q_len ? 0 : rho0 % s.q_len;
-    block_min_limit = s.seq_len - s.q_len + min_i;
+    block_min_limit = row_limit(s, min_i);
   }
   const int clear_tiles = min(j1, (block_min_limit + 1) / kTileTokens); // tiles j < this are clear
   // Clear iterations need j + 1 clear as well; their count is a multiple of
@@ -480,7 +489,18 @@ __global__ __launch_bounds__(kWaves * 64, D == 128 ? 1 : 2) void paged_prefill_k
   const float ltot = lsum + __shfl_xor(lsum, 32);
   // Lane holds O^T[d][rho] for d = 32n + 8*(e/4) + 4*hh + e%4.
   if (p.kv_splits == 1) {
-    if (valid) {
+    if (valid && p.state_o) {
+      const float inv = 1.f / ltot;
+      const int64_t srow = (int64_t)(h * p.group_size + r) * p.state_tokens + s.q_start + i;
+      float* dst = p.state_o + srow * D;
+#pragma unroll
+      for (int n = 0; n < D / 32; n++)
+#pragma unroll
+        for (int a = 0; a < 4; a++)
+          *reinterpret_cast<float4v*>(dst + 32 * n + 8 * a + 4 * hh) =
+              float4v{o[n][4 * a], o[n][4 * a + 1], o[n][4 * a + 2], o[n][4 * a + 3]} * inv;
+      if (hh == 0) p.state_lse[srow] = m + __log2f(ltot);
+    } else if (valid) {
       const float inv = 1.f / ltot;
       half_t* dst = static_cast<half_t*>(p.out) + (int64_t)(h * p.group_size + r) * p.out_stride_head +
                     (int64_t)(s.q_start + i) * p.out_stride_token;
@@ -510,45 +530,61 @@ __global__ __launch_bounds__(kWaves * 64, D == 128 ? 1 : 2) void paged_prefill_k
   }
 }
 
-// Merges the kv_splits partial results of every block tile.  Empty splits
-// (no visible key) hold m = -inf, l = 0 and weigh nothing.
+// Merges the kv_splits partial results of every block tile:
+//   out = sum_j 2^(m_j - M) o_j / sum_j 2^(m_j - M) l_j.
+// One wavefront per output row (a 256-thread block covers 4 rows of a tile):
+// lane j holds split j's weight, broadcast by readlane while the partial rows
+// stream as one coalesced 4*D-byte row per load.  Empty splits (no visible
+// key) hold m = -inf, l = 0 and weigh nothing.
 template <int D>
 __global__ __launch_bounds__(256) void prefill_merge_kernel(PrefillParams p) {
-  const int tile = blockIdx.x; // (b, h, rt)
+  constexpr int kPer = D / 64;
+  constexpr int kBlocksPerTile = kBlockRows / kWaves;
+  const int tile = blockIdx.x / kBlocksPerTile; // (b, h, rt)
+  const int lr = (blockIdx.x % kBlocksPerTile) * kWaves + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int l = threadIdx.x & 63;
   const int rt = tile % p.row_tiles;
   const int h = (tile / p.row_tiles) % p.num_kv_heads;
   const int b = tile / (p.row_tiles * p.num_kv_heads);
   const SeqRows s = load_rows(p, b);
-  const int rows = p.group_size * s.q_len;
+  const int rho = rt * kBlockRows + lr;
+  if (rho >= p.group_size * s.q_len) return;
   const int n_tiles = block_key_tiles(s, p.group_size, rt);
   if (n_tiles == 0) return;
   const int tiles_per_split = (n_tiles + p.kv_splits - 1) / p.kv_splits;
-  const int n_parts = (n_tiles + tiles_per_split - 1) / tiles_per_split; // splits that ran
-  const int64_t slot0 = (int64_t)tile * p.kv_splits;
-  for (int w = threadIdx.x; w < kBlockRows * (D / 4); w += blockDim.x) {
-    const int lr = w / (D / 4);
-    const int d4 = (w % (D / 4)) * 4;
-    const int rho = rt * kBlockRows + lr;
-    if (rho >= rows) continue;
-    float mmax = -INFINITY;
-    for (int pp = 0; pp < n_parts; pp++) mmax = fmaxf(mmax, p.partial_ml[((slot0 + pp) * kBlockRows + lr) * 2]);
-    const float m_use = mmax == -INFINITY ? 0.f : mmax;
-    float4v acc = {0.f, 0.f, 0.f, 0.f};
-    float den = 0.f;
-    for (int pp = 0; pp < n_parts; pp++) {
-      const int64_t prow = (slot0 + pp) * kBlockRows + lr;
-      const float mp = p.partial_ml[prow * 2];
-      const float wgt = mp == -INFINITY ? 0.f : exp2f(mp - m_use);
-      den += wgt * p.partial_ml[prow * 2 + 1];
-      acc += wgt * *reinterpret_cast<const float4v*>(p.partial_o + prow * D + d4);
-    }
-    const int r = rho / s.q_len, i = rho % s.q_len;
-    half_t* dst = static_cast<half_t*>(p.out) + (int64_t)(h * p.group_size + r) * p.out_stride_head +
-                  (int64_t)(s.q_start + i) * p.out_stride_token + d4;
-    const float inv = 1.f / den;
+  const int n_parts = (n_tiles + tiles_per_split - 1) / tiles_per_split; // splits that ran (<= 8 < 64 lanes)
+  const int64_t prow0 = (int64_t)tile * p.kv_splits * kBlockRows + lr;  // split j: prow0 + j * kBlockRows
+  const float mj = l < n_parts ? p.partial_ml[(prow0 + (int64_t)l * kBlockRows) * 2] : -INFINITY;
+  float mmax = mj;
 #pragma unroll
-    for (int e = 0; e < 4; e++) dst[e] = (half_t)(acc[e] * inv);
+  for (int off = 32; off >= 1; off >>= 1) mmax = fmaxf(mmax, __shfl_xor(mmax, off));
+  const float m_use = mmax == -INFINITY ? 0.f : mmax;
+  const float w = mj == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mj - m_use);
+  float den = l < n_parts ? w * p.partial_ml[(prow0 + (int64_t)l * kBlockRows) * 2 + 1] : 0.f;
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) den += __shfl_xor(den, off);
+  float acc[kPer];
+#pragma unroll
+  for (int e = 0; e < kPer; e++) acc[e] = 0.f;
+  for (int j = 0; j < n_parts; j++) {
+    const float wj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), j));
+    const float* src = p.partial_o + (prow0 + (int64_t)j * kBlockRows) * D + l * kPer;
+#pragma unroll
+    for (int e = 0; e < kPer; e++) acc[e] = fmaf(wj, src[e], acc[e]);
   }
+  const int r = rho / s.q_len, i = rho % s.q_len;
+  const float inv = 1.f / den;
+  if (p.state_o) {
+    const int64_t srow = (int64_t)(h * p.group_size + r) * p.state_tokens + s.q_start + i;
+#pragma unroll
+    for (int e = 0; e < kPer; e++) p.state_o[srow * D + l * kPer + e] = acc[e] * inv;
+    if (l == 0) p.state_lse[srow] = m_use + __log2f(den);
+    return;
+  }
+  half_t* dst = static_cast<half_t*>(p.out) + (int64_t)(h * p.group_size + r) * p.out_stride_head +
+                (int64_t)(s.q_start + i) * p.out_stride_token + l * kPer;
+#pragma unroll
+  for (int e = 0; e < kPer; e++) dst[e] = (half_t)(acc[e] * inv);
 }
 
 template <int D>
@@ -560,7 +596,8 @@ hipError_t launch_typed(const PrefillParams& params, hipStream_t stream) {
   hipLaunchKernelGGL(paged_prefill_kernel<D>, dim3((unsigned)blocks), dim3(kWaves * 64), 0, stream, params);
   hipError_t err = hipGetLastError();
   if (err != hipSuccess || params.kv_splits == 1) return err;
-  hipLaunchKernelGGL(prefill_merge_kernel<D>, dim3(pairs * params.row_tiles), dim3(256), 0, stream, params);
+  hipLaunchKernelGGL(prefill_merge_kernel<D>, dim3(pairs * params.row_tiles * (kBlockRows / kWaves)), dim3(256), 0,
+                     stream, params);
   return hipGetLastError();
 }
 

@@ -28,6 +28,12 @@ struct PrefillParams {
   int32_t row_tiles;  // 128-row tiles per (sequence, kv head)
   int32_t kv_splits; // key-range splits per row tile
   float scale_log2;
+  // Cascade prefix pass (optional): keys [0, key_end[b]) only, all visible to
+  // every row; results as normalised fp32 rows + log2-sum-exp.
+  const int32_t* key_end;
+  float* state_o;   // [q head][state_tokens][D]
+  float* state_lse; // [q head][state_tokens]
+  int32_t state_tokens;
 };
 
 hipError_t launch_paged_prefill(const PrefillParams& params, int head_dim, hipStream_t stream);

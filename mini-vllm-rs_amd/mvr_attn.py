@@ -53,6 +53,9 @@ EXPORTED_SYMBOLS = (
     "mvr_reconstruct_contiguous",
     "mvr_rope_append",
     "mvr_rope_append_validate",
+    "mvr_paged_attention_cascade",
+    "mvr_paged_attention_cascade_workspace_size",
+    "mvr_paged_attention_cascade_validate",
 )
 
 
@@ -113,6 +116,19 @@ class PagedCacheLayoutC(ctypes.Structure):
         ("num_page_ids", ctypes.c_int32),
         ("per_page_token_count", ctypes.c_int32),
         ("cached_token_count", ctypes.c_int32),
+    ]
+
+
+class CascadeGroups(ctypes.Structure):
+    _fields_ = [
+        ("num_groups", ctypes.c_int32),
+        ("max_group_q_len", ctypes.c_int32),
+        ("max_prefix_len", ctypes.c_int32),
+        ("group_cu_q_lens", ctypes.c_void_p),
+        ("group_prefix_lens", ctypes.c_void_p),
+        ("group_block_tables", ctypes.c_void_p),
+        ("seq_prefix_lens", ctypes.c_void_p),
+        ("sum_prefix_lens", ctypes.c_int64),
     ]
 
 
@@ -193,6 +209,14 @@ def load_library():
     lib.mvr_rope_append_validate.restype = ctypes.c_int
     lib.mvr_rope_append_validate.argtypes = [ctypes.POINTER(RopeAppendArgs), ctypes.c_void_p, ctypes.c_void_p,
                                              ctypes.c_void_p, ctypes.c_void_p]
+    lib.mvr_paged_attention_cascade.restype = ctypes.c_int
+    lib.mvr_paged_attention_cascade.argtypes = [ctypes.POINTER(PagedAttentionArgs), ctypes.POINTER(CascadeGroups)]
+    lib.mvr_paged_attention_cascade_workspace_size.restype = ctypes.c_size_t
+    lib.mvr_paged_attention_cascade_workspace_size.argtypes = [ctypes.POINTER(PagedAttentionArgs),
+                                                               ctypes.POINTER(CascadeGroups)]
+    lib.mvr_paged_attention_cascade_validate.restype = ctypes.c_int
+    lib.mvr_paged_attention_cascade_validate.argtypes = [ctypes.POINTER(PagedAttentionArgs),
+                                                         ctypes.POINTER(CascadeGroups)] + [ctypes.c_void_p] * 7
     if lib.mvr_abi_version() != 1:
         raise RuntimeError("libmvr_attn.so ABI version mismatch")
     _lib = lib
@@ -426,3 +450,61 @@ def validate_rope_append(args: RopeAppendArgs, block_tables_host=None, seq_lens_
 
     _check(load_library().mvr_rope_append_validate(ctypes.byref(args), ptr(block_tables_host), ptr(seq_lens_host),
                                                    ptr(cu_q_lens_host), ptr(page_writable_host, np.uint8)))
+
+
+def make_cascade_groups(group_cu_q_lens, group_prefix_lens, group_block_tables, seq_prefix_lens, *,
+                        max_group_q_len: int, max_prefix_len: int, sum_prefix_lens: int = 0) -> CascadeGroups:
+    """Prefix groups for paged_attention_cascade: device int32 tensors (group tensors may be None when there is no
+    group); members of a group are consecutive sequences."""
+    g = CascadeGroups()
+    g.num_groups = 0 if group_prefix_lens is None else int(group_prefix_lens.numel())
+    g.max_group_q_len = max_group_q_len
+    g.max_prefix_len = max_prefix_len
+    g.group_cu_q_lens = group_cu_q_lens.data_ptr() if group_cu_q_lens is not None else None
+    g.group_prefix_lens = group_prefix_lens.data_ptr() if group_prefix_lens is not None else None
+    g.group_block_tables = group_block_tables.data_ptr() if group_block_tables is not None else None
+    g.seq_prefix_lens = seq_prefix_lens.data_ptr()
+    g.sum_prefix_lens = int(sum_prefix_lens)
+    return g
+
+
+def paged_attention_cascade(q, key_pool, value_pool, block_tables, seq_lens, cu_q_lens, groups: CascadeGroups,
+                            out=None, *, max_q_len: int, max_seq_len: int, scale: float = 0.0, workspace=None,
+                            stream=None, sum_seq_lens: int = 0):
+    """paged_attention with each group's shared prefix attended once; returns out [Hq, total_q, D]."""
+    torch = _torch()
+    if out is None:
+        out = torch.empty_like(q, memory_format=torch.contiguous_format)
+    a = make_args(q, key_pool, value_pool, block_tables, seq_lens, cu_q_lens, out, max_q_len=max_q_len,
+                  max_seq_len=max_seq_len, scale=scale, stream=stream, sum_seq_lens=sum_seq_lens)
+    lib = load_library()
+    need = int(lib.mvr_paged_attention_cascade_workspace_size(ctypes.byref(a), ctypes.byref(groups)))
+    if need == 0:
+        _check(lib.mvr_paged_attention_cascade(ctypes.byref(a), ctypes.byref(groups)))  # raises with the reason
+    if workspace is None or workspace.numel() * workspace.element_size() < need:
+        workspace = new_workspace(need, q.device)
+    a.workspace = workspace.data_ptr()
+    a.workspace_bytes = workspace.numel() * workspace.element_size()
+    _check(lib.mvr_paged_attention_cascade(ctypes.byref(a), ctypes.byref(groups)))
+    return out
+
+
+def validate_cascade(args: PagedAttentionArgs, groups: CascadeGroups, block_tables_host=None, seq_lens_host=None,
+                     cu_q_lens_host=None, group_cu_q_lens_host=None, group_prefix_lens_host=None,
+                     group_block_tables_host=None, seq_prefix_lens_host=None) -> None:
+    """Host-side checks of the prefix groups (numpy int32 arrays or None); raises MvrError."""
+    import numpy as np
+
+    keep = []
+
+    def ptr(x):
+        if x is None:
+            return None
+        x = np.ascontiguousarray(x, dtype=np.int32)
+        keep.append(x)
+        return x.ctypes.data
+
+    _check(load_library().mvr_paged_attention_cascade_validate(
+        ctypes.byref(args), ctypes.byref(groups), ptr(block_tables_host), ptr(seq_lens_host), ptr(cu_q_lens_host),
+        ptr(group_cu_q_lens_host), ptr(group_prefix_lens_host), ptr(group_block_tables_host),
+        ptr(seq_prefix_lens_host)))

@@ -40,6 +40,8 @@ class Workload:
     seed: int
     shared_pages: int = 0      # pages read by more than one sequence (counted once in unique bytes)
     notes: str = ""
+    # Groups of consecutive sequences sharing their first pages: (first_seq, n_seqs, prefix_tokens).
+    prefix_groups: List = field(default_factory=list)
 
     @property
     def num_seqs(self) -> int:
@@ -177,7 +179,8 @@ def llama3_8b_spec_verify_f16() -> Workload:
         used += private[s]
     # Each group's prefix pages are read by 4 sequences; 3 of the 4 reads are repeats.
     return Workload("llama3-8b spec-verify f16 b16 q5 ctxU[1024,16384] shared-prefix", "f16", 32, 8, 128, 16,
-                    num_pages, 0.3, seq_lens, np.full(16, q, np.int32), bt, seed, shared_pages=12 * shared)
+                    num_pages, 0.3, seq_lens, np.full(16, q, np.int32), bt, seed, shared_pages=12 * shared,
+                    prefix_groups=[(4 * g, 4, 1024) for g in range(4)])
 
 
 CONFIGS = {
@@ -240,3 +243,17 @@ def device_tensors(w: Workload, values: Optional[tuple] = None, device: str = "c
     sl = torch.from_numpy(w.seq_lens).to(device)
     cu = torch.from_numpy(w.cu_q_lens).to(device)
     return dict(q=q, key_pool=k, value_pool=v, block_tables=bt, seq_lens=sl, cu_q_lens=cu)
+
+
+def cascade_tables(w: Workload):
+    """Host arrays describing w.prefix_groups for cascade attention: group_cu_q_lens, group_prefix_lens,
+    group_block_tables, seq_prefix_lens (int32)."""
+    cu = w.cu_q_lens
+    groups = w.prefix_groups
+    gcu = np.array([cu[g[0]] for g in groups] + [cu[groups[-1][0] + groups[-1][1]]], np.int32)
+    gpre = np.array([g[2] for g in groups], np.int32)
+    gbt = np.stack([w.block_tables[g[0]] for g in groups]).astype(np.int32)
+    spre = np.zeros(w.num_seqs, np.int32)
+    for first, n, pre in groups:
+        spre[first:first + n] = pre
+    return gcu, gpre, gbt, spre

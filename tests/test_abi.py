@@ -207,6 +207,61 @@ def test_rope_append_validate_mirrors_reference_errors():
         M.validate_rope_append(a, bt, [10, 6], [0, 3, 4])
 
 
+def _groups(**kw):
+    g = M.CascadeGroups()
+    g.num_groups = 1
+    g.max_group_q_len = 2
+    g.max_prefix_len = 32
+    fake = 1 << 20
+    g.group_cu_q_lens = g.group_prefix_lens = g.group_block_tables = g.seq_prefix_lens = fake
+    for k, v in kw.items():
+        setattr(g, k, v)
+    return g
+
+
+def test_cascade_scalar_checks_reject_before_launch():
+    lib = M.load_library()
+    a = _args()
+    for kw, msg in [(dict(seq_prefix_lens=None), "seq_prefix_lens is required"),
+                    (dict(max_prefix_len=4096), "exceeds max_seq_len"),
+                    (dict(num_groups=3), "num_groups 3"),
+                    (dict(group_block_tables=None), "group tables are required")]:
+        rc = lib.mvr_paged_attention_cascade(ctypes.byref(a), ctypes.byref(_groups(**kw)))
+        assert rc == M.MVR_E_INVALID_ARGUMENT, kw
+        assert msg in lib.mvr_last_error().decode(), (kw, lib.mvr_last_error())
+    assert lib.mvr_paged_attention_cascade_workspace_size(ctypes.byref(a), ctypes.byref(_groups())) > 0
+
+
+def test_cascade_validate_checks_the_groups():
+    # two sequences of one token each, 16-token pages; both share the first 32 tokens (2 pages)
+    a = _args(max_q_len=1, max_seq_len=1024)
+    bt = [[7, 9] + list(range(20, 82)), [7, 9] + list(range(100, 162))]
+    seq_lens, cu = [200, 300], [0, 1, 2]
+    gbt = [bt[0]]
+    ok = dict(group_cu_q_lens_host=[0, 2], group_prefix_lens_host=[32], group_block_tables_host=gbt,
+              seq_prefix_lens_host=[32, 32])
+    M.validate_cascade(a, _groups(), bt, seq_lens, cu, **ok)
+    bad = [(dict(group_prefix_lens_host=[24]), "not a multiple of page_size"),
+           (dict(group_cu_q_lens_host=[1, 2]), "sequence 0 is in no group"),
+           (dict(seq_prefix_lens_host=[32, 16]), "its group's prefix is 32"),
+           (dict(group_block_tables_host=[[7, 8] + bt[0][2:]]), "differs from its group's shared page")]
+    for change, msg in bad:
+        kw = dict(ok)
+        kw.update(change)
+        with pytest.raises(M.MvrError, match=msg):
+            M.validate_cascade(a, _groups(), bt, seq_lens, cu, **kw)
+    with pytest.raises(M.MvrError, match="exceeds sequence 0's 0 cached tokens"):
+        M.validate_cascade(a, _groups(), bt, [1, 300], cu, **ok)
+    with pytest.raises(M.MvrError, match="is in no group"):
+        M.validate_cascade(a, _groups(num_groups=0), bt, seq_lens, cu, group_cu_q_lens_host=[0],
+                           seq_prefix_lens_host=[0, 32])
+    # a group must begin and end on sequence boundaries (sequence 0 holds packed tokens 0 and 1)
+    a2 = _args(max_q_len=2, max_seq_len=1024)
+    with pytest.raises(M.MvrError, match="does not start at a sequence boundary"):
+        M.validate_cascade(a2, _groups(), bt, seq_lens, [0, 2, 3], group_cu_q_lens_host=[1, 3],
+                           group_prefix_lens_host=[32], group_block_tables_host=gbt, seq_prefix_lens_host=[0, 32])
+
+
 def test_workloads_match_stated_sizes():
     import workloads as W
 
