@@ -8,7 +8,8 @@
 //
 // Block = 4 wavefronts = 128 consecutive grouped rows of one (sequence, KV
 // head); the block walks the visible keys in 32-token tiles that all four
-// wavefronts share through LDS (double-buffered, 16 KiB per stage at D=128):
+// wavefronts share through LDS (a ring of kStages stages, 16 KiB per stage at
+// D=128, filled by direct-to-LDS loads):
 //   * K tile: 16-byte chunks, XOR swizzle (chunk ^ row%16), read back with
 //     ds_read_b128 in the v_mfma_f32_32x32x16_f16 A-operand layout
 //     (lane l: token l%32, dims 8*(l/32)+16s);  S^T = K Q^T in D/16 MFMAs;
@@ -21,7 +22,7 @@
 // Blocks of one (sequence, KV head) are mapped onto one XCD (workgroups are
 // dispatched round-robin over the 8 XCDs), so their shared K/V stays in that
 // XCD's L2.  The key range can be split (kv_splits) to fill the device; split
-// results go to the same fp32 partial workspace as the decode kernel.
+// results go to an fp32 partial workspace that prefill_merge_kernel combines.
 #include "paged_prefill.hpp"
 
 #include <math.h>
