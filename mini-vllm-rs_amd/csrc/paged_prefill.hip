@@ -6,10 +6,14 @@
 // contraction (about 950 flop per byte of K/V at q_len 256) and the MFMA
 // pipes, not HBM, set the roofline.
 //
-// Block = 4 wavefronts = 128 consecutive grouped rows of one (sequence, KV
-// head); the block walks the visible keys in 32-token tiles that all four
-// wavefronts share through LDS (a ring of kStages stages, 16 KiB per stage at
-// D=128, filled by direct-to-LDS loads):
+// Block = 8 wavefronts over 128 consecutive grouped rows of one (sequence, KV
+// head): two groups of 4 wavefronts (32 rows each) hold the same rows and
+// take alternating 32-token key tiles, so every SIMD runs two wavefronts
+// without splitting the keys across blocks; at the end group 1 hands its
+// (O, m, l) to group 0 through LDS and group 0 merges and writes.  Each step
+// stages 64 tokens (one tile per group) in LDS through a ring of kStages
+// stages filled by direct-to-LDS loads (16 KiB of K and of V per stage at
+// D=128):
 //   * K tile: 16-byte chunks, XOR swizzle (chunk ^ row%16), read back with
 //     ds_read_b128 in the v_mfma_f32_32x32x16_f16 A-operand layout
 //     (lane l: token l%32, dims 8*(l/32)+16s);  S^T = K Q^T in D/16 MFMAs;
@@ -45,13 +49,21 @@ typedef __attribute__((address_space(4))) int32_t const_i32;
 
 constexpr int kTileTokens = 32;
 constexpr int kRowsPerWave = 32;
-constexpr int kWaves = 4;
-constexpr int kBlockRows = kRowsPerWave * kWaves;
+constexpr int kRowWaves = 4;                        // wavefronts per 128-row group
+constexpr int kGroups = 2;                          // wavefront groups taking alternating key tiles
+constexpr int kWaves = kRowWaves * kGroups;         // wavefronts per block
+constexpr int kSuperTokens = kTileTokens * kGroups; // tokens per LDS stage: one tile per group
+constexpr int kBlockRows = kRowsPerWave * kRowWaves;
+constexpr int kMergeWaves = 4; // wavefronts per block of prefill_merge_kernel
 constexpr int kXcds = 8;
 #ifndef MVR_PREFILL_STAGES
-#define MVR_PREFILL_STAGES 4
+#define MVR_PREFILL_STAGES 2
 #endif
-constexpr int kStages = MVR_PREFILL_STAGES; // LDS stages (4 or 8): the unrolled loop names each statically
+// LDS stages of kSuperTokens tokens (2, 3 or 4; the unrolled loop names each
+// statically).  Measured on the Qwen2-7B prefill chunk: 2, 3 and 4 stages
+// within 1%: the step's loads land under the step's compute.
+constexpr int kStages = MVR_PREFILL_STAGES;
+static_assert(kStages >= 2 && kStages <= 4, "2, 3 or 4 LDS stages");
 constexpr float kRescaleThreshold = 8.0f; // log2 units: p <= 2^8 between rescales
 
 struct SeqRows {
@@ -115,10 +127,10 @@ __device__ __forceinline__ int block_key_tiles(const SeqRows& s, int group_size,
 
 template <int D>
 struct Tile {
-  static constexpr int kChunksPerRow = D / 8;                          // 16-byte chunks per token row
-  static constexpr int kChunks = kTileTokens * kChunksPerRow;          // per K (or V) tile
-  static constexpr int kChunksPerThread = kChunks / (kWaves * 64);     // 2 at D=128, 1 at D=64
-  static constexpr int kElems = kTileTokens * D;
+  static constexpr int kChunksPerRow = D / 8;                      // 16-byte chunks per token row
+  static constexpr int kChunks = kSuperTokens * kChunksPerRow;     // per K (or V) stage
+  static constexpr int kChunksPerThread = kChunks / (kWaves * 64); // 2 at D=128, 1 at D=64
+  static constexpr int kElems = kSuperTokens * D;
   // V: 32-byte pieces per row, XOR-swizzled with the row.  A transposed read
   // is served per half-wavefront: 4 rows x 2 adjacent pieces, which must land
   // in 8 distinct 32-byte bank groups; 2*(row&3) (D=128) spreads the 4 piece
@@ -130,20 +142,25 @@ struct Tile {
 };
 
 template <int D>
-__global__ __launch_bounds__(kWaves * 64, D == 128 ? 1 : 2) void paged_prefill_kernel(PrefillParams p) {
+__global__ __launch_bounds__(kWaves * 64, 1) void paged_prefill_kernel(PrefillParams p) {
   typedef Tile<D> TL;
   // One LDS object per stage and operand: the compiler tracks the
   // direct-to-LDS loads per object, so a read of one stage never waits for
   // the loads still landing in another.
   __shared__ __attribute__((aligned(16))) half_t k_lds0[TL::kElems], k_lds1[TL::kElems], k_lds2[TL::kElems],
-      k_lds3[TL::kElems], k_lds4[TL::kElems], k_lds5[TL::kElems], k_lds6[TL::kElems], k_lds7[TL::kElems];
+      k_lds3[TL::kElems];
   __shared__ __attribute__((aligned(16))) half_t v_lds0[TL::kElems], v_lds1[TL::kElems], v_lds2[TL::kElems],
-      v_lds3[TL::kElems], v_lds4[TL::kElems], v_lds5[TL::kElems], v_lds6[TL::kElems], v_lds7[TL::kElems];
+      v_lds3[TL::kElems];
+  // Group 1 hands its (m, l) to group 0 here after the key loop (its O goes
+  // through the then idle stages).
+  __shared__ float ml_xfer[kRowWaves][2][64];
 
   const int tid = threadIdx.x;
   const int l = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int hh = l >> 5; // lane half: 0 or 1
+  const int rw = wave % kRowWaves;  // rows rw*32 .. +31 of the block
+  const int grp = wave / kRowWaves; // key tiles j0 + 2i + grp
+  const int hh = l >> 5;            // lane half: 0 or 1
 
   // XCD-aware decode of the block index: block x runs on XCD x % 8; all
   // blocks of one (sequence, kv head) pair sit on the same XCD.
@@ -176,12 +193,12 @@ __global__ __launch_bounds__(kWaves * 64, D == 128 ? 1 : 2) void paged_prefill_k
   const int64_t slot = (int64_t)((b * p.num_kv_heads + h) * p.row_tiles + rt) * p.kv_splits + split;
 
   // This lane's query row.
-  const int rho = rt * kBlockRows + wave * kRowsPerWave + (l & 31);
+  const int rho = rt * kBlockRows + rw * kRowsPerWave + (l & 31);
   const bool valid = rho < rows;
   const int r = valid ? rho / s.q_len : 0;
   const int i = valid ? rho % s.q_len : 0;
   const int limit = valid ? row_limit(s, i) : -1;
-  // Largest causal limit among the wave's rows (rows of a wave are contiguous).
+  // Largest and smallest causal limits among the wave's rows.
   int wave_limit = limit;
   for (int off = 1; off < 64; off <<= 1) wave_limit = max(wave_limit, __shfl_xor(wave_limit, off));
   int wave_min_limit = valid ? limit : INT32_MAX;
@@ -215,10 +232,12 @@ __global__ __launch_bounds__(kWaves * 64, D == 128 ? 1 : 2) void paged_prefill_k
   auto page_div = [&](int tok) { return tok >> pshift; };
   auto page_mod = [&](int tok) { return tok & (p.page_size - 1); };
 
-  // Tiles move straight from HBM/L2 into LDS (global_load_lds_dwordx4: lane
-  // i of a wavefront writes 16 bytes at the wavefront's LDS base + 16 i), so
-  // they take no registers and no LDS store instructions.  Wavefront w, step
-  // u fills LDS chunks (u*4 + w)*64 .. +63 of a tile; LDS chunk P holds token
+  // A stage holds the 64 tokens of one step: tile j0 + 2i (group 0) in rows
+  // 0..31 and tile j0 + 2i + 1 (group 1) in rows 32..63.  Tokens move
+  // straight from HBM/L2 into LDS (global_load_lds_dwordx4: lane i of a
+  // wavefront writes 16 bytes at the wavefront's LDS base + 16 i), so they
+  // take no registers and no LDS store instructions.  Wavefront w, step u
+  // fills LDS chunks (u*8 + w)*64 .. +63 of a stage; LDS chunk P holds token
   // row t = P / (D/8), physical chunk P % (D/8), and the lane fetches the
   // logical 16-byte chunk that the K or V swizzle puts there.  The tokens of
   // one (w, u) are 4 (D=128) or 8 (D=64) consecutive tokens of a 16-token
@@ -234,62 +253,85 @@ __global__ __launch_bounds__(kWaves * 64, D == 128 ? 1 : 2) void paged_prefill_k
     ld_k[u] = 8 * (cs ^ TL::kswz(t));
     ld_v[u] = 8 * (2 * ((cs >> 1) ^ TL::vswz(t)) + (cs & 1));
   }
-  // Branch-free: tokens past the call's last key re-read that key,
-  // so every tile issues the same loads.  Those duplicate keys lie past every
-  // row's causal limit (the last tile is a diagonal tile for every wavefront
-  // that sees it), so their scores are masked to -inf, p = 0, and
-  // p * (finite duplicate V) = 0.
-  // Block-table entries of a tile's (w, u) groups, read one iteration before
-  // the tile's loads are issued: a scalar load makes its user wait for
-  // lgkmcnt(0), which would also drain every LDS read in flight, so the
-  // entries are fetched just before a barrier, where lgkmcnt is drained anyway.
+  // Branch-free: tokens past the call's last key re-read that key, so every
+  // stage issues the same loads.  Those duplicate keys lie past every row's
+  // causal limit (the last tile is a diagonal tile for every wavefront that
+  // sees it), so their scores are masked to -inf, p = 0, and p * (finite
+  // duplicate V) = 0.  Block-table entries of a stage's (w, u) groups are
+  // read one step before its loads are issued: a scalar load makes its user
+  // wait for lgkmcnt(0), which would also drain every LDS read in flight, so
+  // the entries are fetched just before a barrier, where lgkmcnt is drained
+  // anyway.
+  const int n_steps = (j1 - j0 + 1) / 2;
+  const int i_last = max(n_steps - 1, 0);
   struct Pages {
     int64_t pg[TL::kChunksPerThread];
   };
-  auto fetch_pages = [&](int j) {
-    Pages r;
+  auto fetch_pages = [&](int si) {
+    Pages pr;
 #pragma unroll
     for (int u = 0; u < TL::kChunksPerThread; u++)
-      r.pg[u] = bt[page_div(min(j * kTileTokens + ld_t0[u], s.key_end - 1))]; // wave-uniform: scalar load
-    return r;
+      pr.pg[u] = bt[page_div(min((j0 + 2 * si) * kTileTokens + ld_t0[u], s.key_end - 1))]; // wave-uniform
+    return pr;
   };
-  auto issue_tile = [&](int j, const Pages& pages, half_t* kb, half_t* vb) {
+  auto issue_stage = [&](int si, const Pages& pages, half_t* kb, half_t* vb) {
 #pragma unroll
     for (int u = 0; u < TL::kChunksPerThread; u++) {
-      const int tg = min(j * kTileTokens + ld_t[u], s.key_end - 1);
+      const int tg = min((j0 + 2 * si) * kTileTokens + ld_t[u], s.key_end - 1);
       const int64_t row = ((pages.pg[u] * p.num_kv_heads + h) * p.page_size + page_mod(tg)) * D;
       const int dst = (u * kWaves + wave) * 64 * 8;
       load_to_lds16(kpool + row + ld_k[u], kb + dst);
       load_to_lds16(vpool + row + ld_v[u], vb + dst);
     }
   };
-  constexpr int kLoadsPerTile = 2 * TL::kChunksPerThread; // per lane
-  half_t* const k_st[8] = {k_lds0, k_lds1, k_lds2, k_lds3, k_lds4, k_lds5, k_lds6, k_lds7};
-  half_t* const v_st[8] = {v_lds0, v_lds1, v_lds2, v_lds3, v_lds4, v_lds5, v_lds6, v_lds7};
+  constexpr int kLoadsPerStage = 2 * TL::kChunksPerThread; // per lane
+  half_t* const k_st[4] = {k_lds0, k_lds1, k_lds2, k_lds3};
+  half_t* const v_st[4] = {v_lds0, v_lds1, v_lds2, v_lds3};
+  // O hand-off through the first two K and V stages: part n (16 values per
+  // lane) of row wave rw at float (((n * 4 + rw) * 16 + e) * 64 + lane) of
+  // their concatenation, 1024 floats per (n, rw).
+  constexpr int kStageFloats = TL::kElems / 2;
+  static_assert((D / 32) * kRowWaves * 1024 <= 4 * kStageFloats, "O hand-off exceeds four stages");
+  auto xfer_o = [&](int n) -> float* {
+    const int f = (n * kRowWaves + rw) * 1024;
+    const int obj = f / kStageFloats;
+    half_t* base = obj == 0 ? k_lds0 : obj == 1 ? k_lds1 : obj == 2 ? v_lds0 : v_lds1;
+    return reinterpret_cast<float*>(base) + (f % kStageFloats);
+  };
 
-  // Per-lane LDS read offsets, loop-invariant.  K: lane reads token l%32,
-  // chunk 2s+hh.  V^T: step u reads rows 16u+4hh+rsub (and +8), 16 columns
-  // at 32n+16*(g16&1)+csub, through the transposing read.
+  // Per-lane LDS read offsets within this group's 32 rows of a stage.  K:
+  // lane reads token l%32, chunk 2s+hh.  V^T: step u reads rows
+  // 16u+4hh+rsub and +8, 16 columns at 32n+16*(g16&1)+csub, through the
+  // transposing read; rows +8 and +16 keep the same swizzle, so they are
+  // immediate offsets.
+  const int gbase = grp * kTileTokens * D;
   int rk[D / 16];
   {
     const int t = l & 31;
 #pragma unroll
-    for (int st = 0; st < D / 16; st++) rk[st] = t * D + 8 * ((2 * st + hh) ^ TL::kswz(t));
+    for (int st = 0; st < D / 16; st++) rk[st] = gbase + t * D + 8 * ((2 * st + hh) ^ TL::kswz(t));
   }
-  int rva[D / 32][2], rvb[D / 32][2];
+  int rv[D / 32];
   {
     const int g16 = l >> 4, qd = l & 15;
     const int rsub = qd >> 2, csub = 4 * (qd & 3);
 #pragma unroll
-    for (int n = 0; n < D / 32; n++)
-#pragma unroll
-      for (int u = 0; u < 2; u++) {
-        const int row_a = 16 * u + 4 * hh + rsub, row_b = row_a + 8;
-        const int col = 32 * n + 16 * (g16 & 1) + csub;
-        rva[n][u] = row_a * D + ((col >> 4) ^ TL::vswz(row_a)) * 16 + (col & 15);
-        rvb[n][u] = row_b * D + ((col >> 4) ^ TL::vswz(row_b)) * 16 + (col & 15);
-      }
+    for (int n = 0; n < D / 32; n++) {
+      const int row_a = 4 * hh + rsub;
+      const int col = 32 * n + 16 * (g16 & 1) + csub;
+      rv[n] = gbase + row_a * D + ((col >> 4) ^ TL::vswz(row_a)) * 16 + (col & 15);
+    }
   }
+  // Loop-variant copies of the offsets: the stage's constant LDS base is then
+  // added per step instead of one hoisted address register per (stage, read).
+  auto lane_offsets = [&](int (&rkx)[D / 16], int (&rvx)[D / 32]) {
+    int z = 0;
+    asm volatile("" : "+s"(z));
+#pragma unroll
+    for (int st = 0; st < D / 16; st++) rkx[st] = rk[st] + z;
+#pragma unroll
+    for (int n = 0; n < D / 32; n++) rvx[n] = rv[n] + z;
+  };
   const float sl2 = p.scale_log2;
 
   // Wave-uniform tile predicates: a tile is visible when some row of this
@@ -298,14 +340,14 @@ __global__ __launch_bounds__(kWaves * 64, D == 128 ? 1 : 2) void paged_prefill_k
   auto visible = [&](int j) { return j < j1 && j * kTileTokens <= wave_limit; };
   auto diagonal = [&](int j) { return j * kTileTokens + kTileTokens - 1 > wave_min_limit; };
 
-  // S^T of the tile in stage buf: D/16 MFMAs, K read straight into the A operand.
-  auto qk = [&](const half_t* kb) {
+  // S^T of this group's tile: D/16 MFMAs, K read straight into the A operand.
+  auto qk = [&](const half_t* kb, const int (&rkx)[D / 16]) {
     float16v acc;
 #pragma unroll
     for (int e = 0; e < 16; e++) acc[e] = 0.f;
 #pragma unroll
     for (int st = 0; st < D / 16; st++)
-      acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(*reinterpret_cast<const half8*>(kb + rk[st]), q[st], acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(*reinterpret_cast<const half8*>(kb + rkx[st]), q[st], acc, 0, 0, 0);
     return acc;
   };
   // Lane holds tokens tok0 + 8*(e/4) + 4*hh + e%4 of row rho.
@@ -317,10 +359,10 @@ __global__ __launch_bounds__(kWaves * 64, D == 128 ? 1 : 2) void paged_prefill_k
   // Scaled row max (log2 units; scale > 0 keeps the order), both lane halves.
   auto row_max = [&](const float16v& sv) {
     float a = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
-    float b = fmaxf(fmaxf(sv[4], sv[5]), fmaxf(sv[6], sv[7]));
+    float bb = fmaxf(fmaxf(sv[4], sv[5]), fmaxf(sv[6], sv[7]));
     float c = fmaxf(fmaxf(sv[8], sv[9]), fmaxf(sv[10], sv[11]));
     float d = fmaxf(fmaxf(sv[12], sv[13]), fmaxf(sv[14], sv[15]));
-    const float mx = fmaxf(fmaxf(a, b), fmaxf(c, d)) * sl2;
+    const float mx = fmaxf(fmaxf(a, bb), fmaxf(c, d)) * sl2;
     const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
     return fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
   };
@@ -351,88 +393,63 @@ __global__ __launch_bounds__(kWaves * 64, D == 128 ? 1 : 2) void paged_prefill_k
   };
   // O^T += V^T P^T over two 16-token steps u; step u uses tokens
   // 16u + 4*hh + {0..3} and 16u + 8 + 4*hh + {0..3} (the ones this lane holds).
-  auto pv = [&](const half_t* vb, const half8 (&pb)[2]) {
+  auto pv = [&](const half_t* vb, const int (&rvx)[D / 32], const half8 (&pb)[2]) {
 #pragma unroll
     for (int n = 0; n < D / 32; n++) {
 #pragma unroll
       for (int u = 0; u < 2; u++) {
-        const short4v ra = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4*)(vb + rva[n][u]));
-        const short4v rb = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4*)(vb + rvb[n][u]));
+        const short4v ra = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4*)(vb + rvx[n] + 16 * D * u));
+        const short4v rb = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4*)(vb + rvx[n] + 16 * D * u + 8 * D));
         const half8 vt = __builtin_bit_cast(half8, __builtin_shufflevector(ra, rb, 0, 1, 2, 3, 4, 5, 6, 7));
         o[n] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vt, pb[u], o[n], 0, 0, 0);
       }
     }
   };
 
-  // Software pipeline over 32-token tiles in kStages LDS stages; the stage of
-  // tile t is (t - j0) % kStages.  Iteration j issues the loads of tile
-  // j + kStages - 1 into the stage that held tile j-1 (released by the
-  // previous barrier), so every tile has kStages - 2 iterations to arrive.
-  // Then, with tile j's scores sc already masked and folded into the running
-  // max:
-  //   block A: S(j+1) = K(j+1) Q^T on the MFMA pipe while the VALU computes
-  //            P(j) = exp2(sc - m) (independent instructions, one basic block);
-  //   block B: O += V(j)^T P(j) on the MFMA pipe while the VALU masks and
-  //            reduces S(j+1);
-  // moves the running max for tile j+1, and the wavefronts meet once tile
-  // j+2 has landed.  Loads past the last tile re-read it (clamped) into
-  // stages nobody reads again.  Measured on the Qwen2-7B prefill chunk: 4
-  // stages 70 us, 8 stages 84 us (more loads in flight slowed the block).
-  constexpr int kAhead = kStages - 1;                        // tiles issued ahead of the one consumed
-  constexpr int kInFlight = (kStages - 3) * kLoadsPerTile;   // loads a barrier leaves in flight
-  const int j_last = max(j1 - 1, j0);
+  // Pipeline over steps of two tiles in kStages LDS stages; step i uses stage
+  // i % kStages.  Step i issues the loads of step i + kStages - 1 into the
+  // stage that held step i - 1 (released by the previous barrier), then each
+  // group attends its tile, and the wavefronts meet once step i + 1 has
+  // landed.  Loads past the last step re-read it (clamped) into stages nobody
+  // reads again.  (Skewing group 1 by half a step, so that its softmax would
+  // fall under group 0's MFMAs, measured slower: 58.4 against 55.7 us.)
+  constexpr int kAhead = kStages - 1;                       // steps issued ahead of the one consumed
+  constexpr int kInFlight = (kStages - 2) * kLoadsPerStage; // loads a barrier leaves in flight
 #pragma unroll
-  for (int a = 0; a < kAhead; a++) {
-    const int t = min(j0 + a, j_last);
-    issue_tile(t, fetch_pages(t), k_st[a], v_st[a]);
-  }
-  Pages next_pages = fetch_pages(min(j0 + kAhead, j_last));
-  tile_barrier<kInFlight + kLoadsPerTile>(); // tiles j0 and j0+1 landed
+  for (int a = 0; a < kAhead; a++) issue_stage(min(a, i_last), fetch_pages(min(a, i_last)), k_st[a], v_st[a]);
+  Pages next_pages = fetch_pages(min(kAhead, i_last));
+  tile_barrier<kInFlight>(); // step 0 landed
 
-  float16v sc;
-#pragma unroll
-  for (int e = 0; e < 16; e++) sc[e] = 0.f;
-  if (visible(j0)) {
-    sc = qk(k_st[0]);
-    if (diagonal(j0)) mask(j0, sc);
-    advance_max(row_max(sc));
-  }
-
-  // Tiles every row of the block sees in full need neither visibility tests
-  // nor masks; while tiles j and j+1 are both such, an iteration is one
-  // branch-free stretch.
-  auto iterate_clear = [&](int j, auto st_c) {
+  // Steps whose two tiles every row of the block sees in full need neither
+  // visibility tests nor masks.
+  auto step_clear = [&](int si, auto st_c) {
     constexpr int st = decltype(st_c)::value;
-    issue_tile(min(j + kAhead, j_last), next_pages, k_st[(st + kAhead) & (kStages - 1)],
-               v_st[(st + kAhead) & (kStages - 1)]);
+    issue_stage(min(si + kAhead, i_last), next_pages, k_st[(st + kAhead) % kStages], v_st[(st + kAhead) % kStages]);
+    int rkx[D / 16], rvx[D / 32];
+    lane_offsets(rkx, rvx);
+    float16v sc = qk(k_st[st], rkx);
+    advance_max(row_max(sc));
     half8 pb[2];
-    const float16v sn = qk(k_st[(st + 1) & (kStages - 1)]);
     exps(sc, pb);
-    pv(v_st[st], pb);
-    advance_max(row_max(sn));
-    sc = sn;
-    next_pages = fetch_pages(min(j + kStages, j_last));
+    pv(v_st[st], rvx, pb);
+    next_pages = fetch_pages(min(si + kStages, i_last));
     tile_barrier<kInFlight>();
   };
-  auto iterate = [&](int j, auto st_c) {
+  auto step = [&](int si, auto st_c) {
     constexpr int st = decltype(st_c)::value;
-    issue_tile(min(j + kAhead, j_last), next_pages, k_st[(st + kAhead) & (kStages - 1)],
-               v_st[(st + kAhead) & (kStages - 1)]);
+    issue_stage(min(si + kAhead, i_last), next_pages, k_st[(st + kAhead) % kStages], v_st[(st + kAhead) % kStages]);
+    const int j = j0 + 2 * si + grp;
     if (visible(j)) {
+      int rkx[D / 16], rvx[D / 32];
+      lane_offsets(rkx, rvx);
+      float16v sc = qk(k_st[st], rkx);
+      if (diagonal(j)) mask(j, sc);
+      advance_max(row_max(sc));
       half8 pb[2];
-      if (visible(j + 1)) {
-        float16v sn = qk(k_st[(st + 1) & (kStages - 1)]);
-        exps(sc, pb);
-        if (diagonal(j + 1)) mask(j + 1, sn);
-        pv(v_st[st], pb);
-        advance_max(row_max(sn));
-        sc = sn;
-      } else {
-        exps(sc, pb);
-        pv(v_st[st], pb);
-      }
+      exps(sc, pb);
+      pv(v_st[st], rvx, pb);
     }
-    next_pages = fetch_pages(min(j + kStages, j_last));
+    next_pages = fetch_pages(min(si + kStages, i_last));
     tile_barrier<kInFlight>();
   };
   // Smallest causal limit among the block's valid rows.
@@ -444,48 +461,67 @@ __global__ __launch_bounds__(kWaves * 64, D == 128 ? 1 : 2) void paged_prefill_k
     block_min_limit = row_limit(s, min_i);
   }
   const int clear_tiles = min(j1, (block_min_limit + 1) / kTileTokens); // tiles j < this are clear
-  // Clear iterations need j + 1 clear as well; their count is a multiple of
-  // kStages so that the general loop starts on stage 0.
-  const int j_mid = j0 + max(0, (clear_tiles - 1 - j0) / kStages * kStages);
+  // Clear steps (both tiles clear); their count is a multiple of kStages so
+  // that the general loop starts on stage 0.
+  const int i_mid = max(0, (clear_tiles - j0) / 2) / kStages * kStages;
 
   // Unrolled by kStages so that every stage is named statically: LDS
   // addresses become immediate offsets and each stage is its own object.
 #define MVR_STAGE(K) std::integral_constant<int, K>()
-  for (int j = j0; j < j_mid; j += kStages) {
-    iterate_clear(j, MVR_STAGE(0));
-    iterate_clear(j + 1, MVR_STAGE(1));
-    iterate_clear(j + 2, MVR_STAGE(2));
-    iterate_clear(j + 3, MVR_STAGE(3));
-    if constexpr (kStages == 8) {
-      iterate_clear(j + 4, MVR_STAGE(4));
-      iterate_clear(j + 5, MVR_STAGE(5));
-      iterate_clear(j + 6, MVR_STAGE(6));
-      iterate_clear(j + 7, MVR_STAGE(7));
-    }
+  for (int si = 0; si < i_mid; si += kStages) {
+    step_clear(si, MVR_STAGE(0));
+    step_clear(si + 1, MVR_STAGE(1));
+    if constexpr (kStages >= 3) step_clear(si + 2, MVR_STAGE(2));
+    if constexpr (kStages == 4) step_clear(si + 3, MVR_STAGE(3));
   }
-  for (int j = j_mid; j < j1; j += kStages) {
-    iterate(j, MVR_STAGE(0));
-    if (j + 1 >= j1) break;
-    iterate(j + 1, MVR_STAGE(1));
-    if (j + 2 >= j1) break;
-    iterate(j + 2, MVR_STAGE(2));
-    if (j + 3 >= j1) break;
-    iterate(j + 3, MVR_STAGE(3));
-    if constexpr (kStages == 8) {
-      if (j + 4 >= j1) break;
-      iterate(j + 4, MVR_STAGE(4));
-      if (j + 5 >= j1) break;
-      iterate(j + 5, MVR_STAGE(5));
-      if (j + 6 >= j1) break;
-      iterate(j + 6, MVR_STAGE(6));
-      if (j + 7 >= j1) break;
-      iterate(j + 7, MVR_STAGE(7));
+  for (int si = i_mid; si < n_steps; si += kStages) {
+    step(si, MVR_STAGE(0));
+    if (si + 1 >= n_steps) break;
+    step(si + 1, MVR_STAGE(1));
+    if constexpr (kStages >= 3) {
+      if (si + 2 >= n_steps) break;
+      step(si + 2, MVR_STAGE(2));
+    }
+    if constexpr (kStages == 4) {
+      if (si + 3 >= n_steps) break;
+      step(si + 3, MVR_STAGE(3));
     }
   }
 #undef MVR_STAGE
-  // Every issued load has landed before the block exits (the last barrier
-  // left up to one tile of clamped re-reads in flight).
+  // Every issued load has landed before the LDS is reused or the block exits
+  // (the last barrier left up to kStages - 2 steps of clamped re-reads in
+  // flight).
   __builtin_amdgcn_s_waitcnt(0x0070); // vmcnt(0) expcnt(7) lgkmcnt(0)
+
+  // Group 1 hands its running state to group 0, which merges:
+  //   M = max(m0, m1), o = 2^(m0-M) o0 + 2^(m1-M) o1, l likewise.
+  // The last barrier of the loop passed after every wavefront's last LDS
+  // read, and the wait above drained the loads, so the stages are free.
+  if (grp == 1) {
+#pragma unroll
+    for (int n = 0; n < D / 32; n++) {
+      float* dst = xfer_o(n);
+#pragma unroll
+      for (int e = 0; e < 16; e++) dst[e * 64 + l] = o[n][e];
+    }
+    ml_xfer[rw][0][l] = m;
+    ml_xfer[rw][1][l] = lsum;
+  }
+  __syncthreads();
+  if (grp == 1) return;
+  {
+    const float m1 = ml_xfer[rw][0][l];
+    const float l1 = ml_xfer[rw][1][l];
+    const float mm = fmaxf(m, m1);
+    const float a0 = m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m - mm);
+    const float a1 = m1 == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m1 - mm);
+#pragma unroll
+    for (int n = 0; n < D / 32; n++)
+#pragma unroll
+      for (int e = 0; e < 16; e++) o[n][e] = a0 * o[n][e] + a1 * xfer_o(n)[e * 64 + l];
+    lsum = a0 * lsum + a1 * l1;
+    m = mm;
+  }
 
   const float ltot = lsum + __shfl_xor(lsum, 32);
   // Lane holds O^T[d][rho] for d = 32n + 8*(e/4) + 4*hh + e%4.
@@ -515,7 +551,7 @@ __global__ __launch_bounds__(kWaves * 64, D == 128 ? 1 : 2) void paged_prefill_k
         }
     }
   } else if (valid) {
-    const int64_t prow = slot * kBlockRows + wave * kRowsPerWave + (l & 31);
+    const int64_t prow = slot * kBlockRows + rw * kRowsPerWave + (l & 31);
     float* dst = p.partial_o + prow * D;
 #pragma unroll
     for (int n = 0; n < D / 32; n++)
@@ -540,9 +576,9 @@ __global__ __launch_bounds__(kWaves * 64, D == 128 ? 1 : 2) void paged_prefill_k
 template <int D>
 __global__ __launch_bounds__(256) void prefill_merge_kernel(PrefillParams p) {
   constexpr int kPer = D / 64;
-  constexpr int kBlocksPerTile = kBlockRows / kWaves;
+  constexpr int kBlocksPerTile = kBlockRows / kMergeWaves;
   const int tile = blockIdx.x / kBlocksPerTile; // (b, h, rt)
-  const int lr = (blockIdx.x % kBlocksPerTile) * kWaves + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lr = (blockIdx.x % kBlocksPerTile) * kMergeWaves + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int l = threadIdx.x & 63;
   const int rt = tile % p.row_tiles;
   const int h = (tile / p.row_tiles) % p.num_kv_heads;
@@ -597,7 +633,7 @@ hipError_t launch_typed(const PrefillParams& params, hipStream_t stream) {
   hipLaunchKernelGGL(paged_prefill_kernel<D>, dim3((unsigned)blocks), dim3(kWaves * 64), 0, stream, params);
   hipError_t err = hipGetLastError();
   if (err != hipSuccess || params.kv_splits == 1) return err;
-  hipLaunchKernelGGL(prefill_merge_kernel<D>, dim3(pairs * params.row_tiles * (kBlockRows / kWaves)), dim3(256), 0,
+  hipLaunchKernelGGL(prefill_merge_kernel<D>, dim3(pairs * params.row_tiles * (kBlockRows / kMergeWaves)), dim3(256), 0,
                      stream, params);
   return hipGetLastError();
 }
