@@ -297,6 +297,9 @@ def _ragged_workload(name, seed, hq, hkv, d, ctx, qlens, page_size=16, dtype="f1
     (8, 2, 64, [300, 1000], [80, 33], 32),              # head_dim 64, page size 32
     (7, 1, 128, [64], [130], 16),                       # a single (sequence, kv head) pair
     (32, 8, 128, [4000, 17, 900], [16, 9, 120], 16),    # decode-sized and prefill-sized requests mixed
+    # The kernel's two wavefront groups take alternating 32-token key tiles and merge at the end:
+    (28, 4, 128, [0, 31], [16, 33], 16),                # one key tile (the second group sees none), two tiles
+    (7, 1, 64, [40], [100], 16),                        # head_dim 64 with an odd number of key tiles
 ])
 def test_prefill_shapes_match_oracle(shape):
     hq, hkv, d, ctx, qlens, P = shape
