@@ -245,6 +245,9 @@ struct CascadePass {
   float* state_o = nullptr;           // normalised fp32 rows instead of `out`
   float* state_lse = nullptr;
   int32_t state_tokens = 0;
+  const float* prefix_o = nullptr;    // suffix pass: merge `out` rows with this prefix state
+  const float* prefix_lse = nullptr;
+  const int32_t* seq_prefix_len = nullptr;
 };
 
 // Launches the planned kernel(s); workspace ws holds plan.partial_bytes.
@@ -252,6 +255,9 @@ int launch_planned(const mvr_paged_attention_args* a, const mvr::PagedAttentionP
                    const CascadePass& cp) {
   const float scale = a->scale > 0.f ? a->scale : (float)(1.0 / sqrt((double)a->head_dim));
   if (plan.prefill) {
+    // The suffix pass is planned on the split-context kernel, which alone
+    // merges rows with a prefix state.
+    if (cp.prefix_o) return fail(MVR_E_INVALID_ARGUMENT, "internal: prefix merge planned on the prefill kernel");
     mvr::PrefillParams f{};
     f.q = a->q;
     f.q_stride_head = a->q_stride_head;
@@ -324,6 +330,9 @@ int launch_planned(const mvr_paged_attention_args* a, const mvr::PagedAttentionP
   p.state_o = cp.state_o;
   p.state_lse = cp.state_lse;
   p.state_tokens = cp.state_tokens;
+  p.prefix_o = cp.prefix_o;
+  p.prefix_lse = cp.prefix_lse;
+  p.seq_prefix_len = cp.seq_prefix_len;
 
   TraceRange launch("attn-paged-fused"); // one launch replaces attn-qk / attn-mask-softmax / attn-paged-v
   hipError_t err = mvr::launch_paged_attention(plan, p, static_cast<hipStream_t>(a->stream));
@@ -341,14 +350,14 @@ int check_workspace(const mvr_paged_attention_args* a, size_t need) {
 
 // Cascade attention: a prefix pass over the groups' shared pages (each
 // group's members' query rows as one virtual sequence whose keys end at the
-// prefix), a suffix pass per sequence from its prefix on, and a merge of the
-// two normalised states.  Workspace: [prefix partials][suffix partials]
-// [state A o][state A lse][state B o][state B lse].
+// prefix) into a normalised fp32 state, then a suffix pass per sequence from
+// its prefix on, whose final write merges each row with that state.
+// Workspace: [prefix partials][suffix partials][prefix o][prefix lse].
 struct CascadePlan {
   mvr_paged_attention_args pre, suf;
   mvr::PagedAttentionPlan pre_plan, suf_plan;
   int32_t state_tokens; // bound of the packed token count: state row stride
-  size_t off_suf, off_a_o, off_a_lse, off_b_o, off_b_lse, total;
+  size_t off_suf, off_a_o, off_a_lse, total;
 };
 
 int check_cascade(const mvr_paged_attention_args* a, const mvr_cascade_groups* g) {
@@ -396,9 +405,7 @@ CascadePlan make_cascade_plan(const mvr_paged_attention_args* a, const mvr_casca
   c.off_suf = align_up(c.pre_plan.partial_bytes, 256);
   c.off_a_o = c.off_suf + align_up(c.suf_plan.partial_bytes, 256);
   c.off_a_lse = c.off_a_o + align_up(so, 256);
-  c.off_b_o = c.off_a_lse + align_up(sl, 256);
-  c.off_b_lse = c.off_b_o + align_up(so, 256);
-  c.total = c.off_b_lse + align_up(sl, 256);
+  c.total = c.off_a_lse + align_up(sl, 256);
   return c;
 }
 
@@ -587,8 +594,6 @@ int mvr_paged_attention_cascade(const mvr_paged_attention_args* a, const mvr_cas
   char* ws = static_cast<char*>(a->workspace);
   float* a_o = reinterpret_cast<float*>(ws + c.off_a_o);
   float* a_lse = reinterpret_cast<float*>(ws + c.off_a_lse);
-  float* b_o = reinterpret_cast<float*>(ws + c.off_b_o);
-  float* b_lse = reinterpret_cast<float*>(ws + c.off_b_lse);
   if (g->num_groups > 0) {
     CascadePass pre;
     pre.key_end = g->group_prefix_lens;
@@ -598,29 +603,16 @@ int mvr_paged_attention_cascade(const mvr_paged_attention_args* a, const mvr_cas
     rc = launch_planned(&c.pre, c.pre_plan, ws, pre);
     if (rc != MVR_OK) return rc;
   }
+  // The suffix pass writes `out`, each row merged with its prefix state.
   CascadePass suf;
   suf.key_begin = g->seq_prefix_lens;
-  suf.state_o = b_o;
-  suf.state_lse = b_lse;
   suf.state_tokens = c.state_tokens;
-  rc = launch_planned(&c.suf, c.suf_plan, ws + c.off_suf, suf);
-  if (rc != MVR_OK) return rc;
-  mvr::PagedAttentionParams p{};
-  p.cu_q_lens = a->cu_q_lens;
-  p.single_q_len = a->max_q_len;
-  p.num_seqs = a->num_seqs;
-  p.num_kv_heads = a->num_kv_heads;
-  p.group_size = a->num_q_heads / a->num_kv_heads;
-  p.out = a->out;
-  p.out_stride_head = a->out_stride_head;
-  p.out_stride_token = a->out_stride_token;
-  p.state_o = b_o;
-  p.state_lse = b_lse;
-  p.state_tokens = c.state_tokens;
-  hipError_t err = mvr::launch_merge_states(p, a->dtype, a->head_dim, a_o, a_lse, g->seq_prefix_lens, c.state_tokens,
-                                            static_cast<hipStream_t>(a->stream));
-  if (err != hipSuccess) return fail(MVR_E_HIP, "kernel launch failed: %s", hipGetErrorString(err));
-  return MVR_OK;
+  if (g->num_groups > 0) {
+    suf.prefix_o = a_o;
+    suf.prefix_lse = a_lse;
+    suf.seq_prefix_len = g->seq_prefix_lens;
+  }
+  return launch_planned(&c.suf, c.suf_plan, ws + c.off_suf, suf);
 }
 
 int mvr_paged_attention_cascade_validate(const mvr_paged_attention_args* a, const mvr_cascade_groups* g,

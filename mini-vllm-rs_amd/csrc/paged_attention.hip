@@ -102,6 +102,23 @@ __device__ __forceinline__ int tile_parts(const SeqInfo& s, int n_chunks, int ch
   return n_chunks > kb ? (n_chunks - kb + chunks_per_part - 1) / chunks_per_part : 0;
 }
 
+// Cascade suffix pass: weights that merge this pass's normalised row (log2
+// sum lb) with the prefix pass's state of the same row (srow):
+//   out = (wa * o_a + wb * o_b) * inv.
+// `has` is false when the row's sequence has no prefix (its prefix state was
+// never written and must not be read).
+struct PrefixWeights {
+  bool has;
+  float wa, wb, inv;
+};
+__device__ __forceinline__ PrefixWeights prefix_weights(const PagedAttentionParams& p, int b, int64_t srow, float lb) {
+  if (!p.prefix_o || ((const const_i32*)p.seq_prefix_len)[b] <= 0) return {false, 0.f, 1.f, 1.f};
+  const float la = p.prefix_lse[srow];
+  const float mx = fmaxf(la, lb);
+  const float wa = exp2f(la - mx), wb = exp2f(lb - mx);
+  return {true, wa, wb, 1.f / (wa + wb)};
+}
+
 // ---------------------------------------------------------------------------
 // dtype traits: how a 16-token chunk is loaded, multiplied and staged.
 // ---------------------------------------------------------------------------
@@ -418,8 +435,19 @@ __global__ __launch_bounds__(kWaveSize* kWavesPerBlock, Tr::template min_blocks<
         } else {
           T* dst =
               static_cast<T*>(p.out) + (int64_t)q_head[nb] * p.out_stride_head + (int64_t)q_tok[nb] * p.out_stride_token;
+          const int64_t srow = (int64_t)q_head[nb] * p.state_tokens + q_tok[nb];
+          const PrefixWeights pw = prefix_weights(p, b, srow, m[nb] + __log2f(ltot));
+          if (pw.has) {
+            const float* src = p.prefix_o + srow * D;
 #pragma unroll
-          for (int n = 0; n < D / 16; n++) Tr::store_out(dst + 16 * n + 4 * g, o[nb][n] * inv);
+            for (int n = 0; n < D / 16; n++)
+              Tr::store_out(dst + 16 * n + 4 * g,
+                            (pw.wa * *reinterpret_cast<const float4v*>(src + 16 * n + 4 * g) + pw.wb * (o[nb][n] * inv)) *
+                                pw.inv);
+          } else {
+#pragma unroll
+            for (int n = 0; n < D / 16; n++) Tr::store_out(dst + 16 * n + 4 * g, o[nb][n] * inv);
+          }
         }
       }
     } else {
@@ -520,57 +548,16 @@ __global__ __launch_bounds__(256) void merge_partitions_kernel(PagedAttentionPar
   }
   T* dst = static_cast<T*>(p.out) + (int64_t)(h * p.group_size + r) * p.out_stride_head +
            (int64_t)(s.q_start + i) * p.out_stride_token + l * kPer;
+  const int64_t srow = (int64_t)(h * p.group_size + r) * p.state_tokens + s.q_start + i;
+  const PrefixWeights pw = prefix_weights(p, b, srow, m_use + __log2f(den));
+  if (pw.has) {
+    const float* src = p.prefix_o + srow * D + l * kPer;
+#pragma unroll
+    for (int e = 0; e < kPer; e++) dst[e] = (T)((pw.wa * src[e] + pw.wb * (acc[e] * inv)) * pw.inv);
+    return;
+  }
 #pragma unroll
   for (int e = 0; e < kPer; e++) dst[e] = (T)(acc[e] * inv);
-}
-
-// Cascade merge of two attention states per output row (q head, packed
-// token): A from the shared-prefix pass (sequences in a prefix group only),
-// B from the suffix pass; out = (2^(lse_a - M) o_a + 2^(lse_b - M) o_b) /
-// (2^(lse_a - M) + 2^(lse_b - M)).  One wavefront per row; total_q bounds
-// the packed token count (rows past cu_q_lens[num_seqs] exit).
-template <typename T, int D>
-__global__ __launch_bounds__(256) void merge_states_kernel(PagedAttentionParams p, const float* a_o,
-                                                           const float* a_lse, const int32_t* seq_prefix_len,
-                                                           int32_t total_q) {
-  constexpr int kPer = D / kWaveSize;
-  const int64_t row = (int64_t)blockIdx.x * kWavesPerBlock + __builtin_amdgcn_readfirstlane(threadIdx.x / kWaveSize);
-  const int hq = p.num_kv_heads * p.group_size;
-  const int qh = (int)(row / total_q);
-  const int n = (int)(row - (int64_t)qh * total_q);
-  if (qh >= hq) return;
-  // total_q is a host-side bound; tokens past the real packed count exit.
-  const const_i32* cu = (const const_i32*)p.cu_q_lens;
-  if (n >= (p.cu_q_lens ? cu[p.num_seqs] : p.single_q_len)) return;
-  int b = 0;
-  if (p.cu_q_lens) { // largest b with cu_q_lens[b] <= n: uniform, scalar loads
-    int lo = 0, hi = p.num_seqs - 1;
-    while (lo < hi) {
-      const int mid = (lo + hi + 1) >> 1;
-      if (cu[mid] <= n)
-        lo = mid;
-      else
-        hi = mid - 1;
-    }
-    b = lo;
-  }
-  const bool has_prefix = ((const const_i32*)seq_prefix_len)[b] > 0;
-  const int l = lane_id();
-  const int64_t srow = (int64_t)qh * p.state_tokens + n;
-  float out[kPer];
-#pragma unroll
-  for (int e = 0; e < kPer; e++) out[e] = p.state_o[srow * D + l * kPer + e];
-  if (has_prefix) {
-    const float la = a_lse[srow], lb = p.state_lse[srow];
-    const float mx = fmaxf(la, lb);
-    const float wa = exp2f(la - mx), wb = exp2f(lb - mx);
-    const float inv = 1.f / (wa + wb);
-#pragma unroll
-    for (int e = 0; e < kPer; e++) out[e] = (wa * a_o[srow * D + l * kPer + e] + wb * out[e]) * inv;
-  }
-  T* dst = static_cast<T*>(p.out) + (int64_t)qh * p.out_stride_head + (int64_t)n * p.out_stride_token + l * kPer;
-#pragma unroll
-  for (int e = 0; e < kPer; e++) dst[e] = (T)out[e];
 }
 
 template <typename Tr, int D, int NB>
@@ -607,28 +594,6 @@ hipError_t launch_paged_attention(const PagedAttentionPlan& plan, PagedAttention
     MVR_DISPATCH(F32Traits, 128, 2)
   }
 #undef MVR_DISPATCH
-  return hipErrorInvalidValue;
-}
-
-hipError_t launch_merge_states(const PagedAttentionParams& p, int dtype, int head_dim, const float* prefix_o,
-                               const float* prefix_lse, const int32_t* seq_prefix_len, int32_t total_q,
-                               hipStream_t stream) {
-  const int64_t rows = (int64_t)p.num_kv_heads * p.group_size * total_q;
-  const dim3 grid((unsigned)((rows + kWavesPerBlock - 1) / kWavesPerBlock)), block(kWaveSize * kWavesPerBlock);
-#define MVR_MERGE(T, DD)                                                                                        \
-  if (head_dim == DD) {                                                                                         \
-    hipLaunchKernelGGL((merge_states_kernel<T, DD>), grid, block, 0, stream, p, prefix_o, prefix_lse, seq_prefix_len, \
-                       total_q);                                                                                \
-    return hipGetLastError();                                                                                   \
-  }
-  if (dtype == 1) {
-    MVR_MERGE(half_t, 64)
-    MVR_MERGE(half_t, 128)
-  } else {
-    MVR_MERGE(float, 64)
-    MVR_MERGE(float, 128)
-  }
-#undef MVR_MERGE
   return hipErrorInvalidValue;
 }
 

@@ -43,6 +43,12 @@ struct PagedAttentionParams {
   float* state_o;           // write normalised fp32 rows [q head][state_tokens][D] instead of `out` ...
   float* state_lse;         // ... and their log2-sum-exp [q head][state_tokens]
   int32_t state_tokens;
+  // Cascade suffix pass (optional): before a row of `out` is written, it is
+  // merged with the prefix pass's state of that row, for sequences whose
+  // seq_prefix_len is > 0:  out = (2^(la-M) o_a + 2^(lb-M) o_b) / (2^(la-M) + 2^(lb-M)).
+  const float* prefix_o;          // [q head][state_tokens][D], normalised
+  const float* prefix_lse;        // [q head][state_tokens], log2 units
+  const int32_t* seq_prefix_len;  // [num_seqs]
 };
 
 // Grid shape chosen by the host.
@@ -61,13 +67,6 @@ struct PagedAttentionPlan {
 
 hipError_t launch_paged_attention(const PagedAttentionPlan& plan, PagedAttentionParams params, hipStream_t stream);
 
-// Cascade merge: out[q head][token] from the prefix-pass state (prefix_o,
-// prefix_lse; used where seq_prefix_len of the token's sequence is > 0) and
-// the suffix-pass state in params.state_o / state_lse; total_q bounds the
-// packed token count.
-hipError_t launch_merge_states(const PagedAttentionParams& params, int dtype, int head_dim, const float* prefix_o,
-                               const float* prefix_lse, const int32_t* seq_prefix_len, int32_t total_q,
-                               hipStream_t stream);
 
 // Wavefronts of the plan's kernel variant the current device holds at once
 // (occupancy x waves per block x CUs); 0 if the device cannot be queried.

@@ -479,13 +479,14 @@ __global__ __launch_bounds__(kWaves * 64, 1) void paged_prefill_kernel(PrefillPa
 #undef MVR_STAGE
   // Every issued load has landed before the LDS is reused or the block exits
   // (the last barrier left up to kStages - 2 steps of clamped re-reads in
-  // flight).
+  // flight).  Each wavefront waits for its own loads; the barrier then
+  // makes sure no wavefront's loads still land in the stages that carry the
+  // hand-off below.
   __builtin_amdgcn_s_waitcnt(0x0070); // vmcnt(0) expcnt(7) lgkmcnt(0)
+  __syncthreads();
 
   // Group 1 hands its running state to group 0, which merges:
   //   M = max(m0, m1), o = 2^(m0-M) o0 + 2^(m1-M) o1, l likewise.
-  // The last barrier of the loop passed after every wavefront's last LDS
-  // read, and the wait above drained the loads, so the stages are free.
   if (grp == 1) {
 #pragma unroll
     for (int n = 0; n < D / 32; n++) {

@@ -287,6 +287,9 @@ def make_args(q, key_pool, value_pool, block_tables, seq_lens, cu_q_lens, out, *
     a.out_stride_token = out.stride(1)
     a.stream = _stream_handle(stream)
     a.sum_seq_lens = int(sum_seq_lens)
+    # The struct holds raw device addresses: keep the tensors alive with it, so that a table built inline
+    # (make_args(..., torch.tensor(...).cuda(), ...)) is not freed and its memory reused before the launch.
+    a._keep = (q, key_pool, value_pool, block_tables, seq_lens, cu_q_lens, out)
     return a
 
 
@@ -418,6 +421,7 @@ def make_rope_append_args(q, k, v, cos_table, sin_table, block_tables, seq_lens,
     a.key_pool = key_pool.data_ptr()
     a.value_pool = value_pool.data_ptr()
     a.stream = _stream_handle(stream)
+    a._keep = (q, k, v, cos_table, sin_table, block_tables, seq_lens, cu_q_lens, q_out, key_pool, value_pool)
     return a
 
 
@@ -465,6 +469,9 @@ def make_cascade_groups(group_cu_q_lens, group_prefix_lens, group_block_tables, 
     g.group_block_tables = group_block_tables.data_ptr() if group_block_tables is not None else None
     g.seq_prefix_lens = seq_prefix_lens.data_ptr()
     g.sum_prefix_lens = int(sum_prefix_lens)
+    # Raw device addresses: keep the tables alive with the struct (tables passed as temporaries would
+    # otherwise be freed, and their memory reused, e.g. by the call's own output, before the kernels read them).
+    g._keep = (group_cu_q_lens, group_prefix_lens, group_block_tables, seq_prefix_lens)
     return g
 
 

@@ -207,6 +207,40 @@ def test_rope_append_validate_mirrors_reference_errors():
         M.validate_rope_append(a, bt, [10, 6], [0, 3, 4])
 
 
+def test_argument_structs_keep_their_tensors_alive():
+    # The structs carry raw addresses.  Tables passed as temporaries must live as long as the struct: freed,
+    # their memory can be reused (by the call's own output, say) before the kernels read them.
+    import gc
+    import weakref
+
+    torch = pytest.importorskip("torch")
+    refs = []
+
+    def tmp(*shape, dtype=torch.int32):
+        t = torch.zeros(*shape, dtype=dtype)
+        refs.append(weakref.ref(t))
+        return t
+
+    class NullStream:  # no launch happens here: any handle will do
+        cuda_stream = 0
+
+    g = M.make_cascade_groups(tmp(3), tmp(2), tmp(2, 4), tmp(4), max_group_q_len=2, max_prefix_len=32)
+    a = M.make_args(tmp(8, 4, 64, dtype=torch.float16), tmp(16, 1, 2, 16, 64, dtype=torch.float16),
+                    tmp(16, 1, 2, 16, 64, dtype=torch.float16), tmp(4, 4), tmp(4), tmp(5),
+                    tmp(8, 4, 64, dtype=torch.float16), max_q_len=1, max_seq_len=64, stream=NullStream())
+    r = M.make_rope_append_args(tmp(8, 4, 64, dtype=torch.float16), tmp(2, 4, 64, dtype=torch.float16),
+                                tmp(2, 4, 64, dtype=torch.float16), tmp(64, 32, dtype=torch.float16),
+                                tmp(64, 32, dtype=torch.float16), tmp(4, 4), tmp(4), tmp(5),
+                                tmp(16, 1, 2, 16, 64, dtype=torch.float16), tmp(16, 1, 2, 16, 64, dtype=torch.float16),
+                                tmp(8, 4, 64, dtype=torch.float16), max_seq_len=64, stream=NullStream())
+    gc.collect()
+    assert all(w() is not None for w in refs), "a tensor behind a struct address was freed"
+    assert g.seq_prefix_lens == g._keep[3].data_ptr() and a.cu_q_lens == a._keep[5].data_ptr()
+    del g, a, r
+    gc.collect()
+    assert all(w() is None for w in refs)
+
+
 def _groups(**kw):
     g = M.CascadeGroups()
     g.num_groups = 1
