@@ -217,6 +217,8 @@ def main():
     ap.add_argument("--only-headline", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run 3 device copies of 1 GiB (a plain copy kernel of known size, for HBM counters)")
+    ap.add_argument("--only-config", type=int, default=0, choices=(0, 1, 2, 4, 5),
+                    help="time only this one of the other workloads and print its result (for profiling one kernel)")
     a = ap.parse_args()
     if a.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {a.gpus} is not supported (this path is single-GPU; "
@@ -232,6 +234,11 @@ def main():
         print("no GPU visible", file=sys.stderr)
         sys.exit(1)
     M.load_library()
+    if a.only_config:
+        log(f"[bench] config {a.only_config} only")
+        res = measure(W, M, torch, a.only_config, a.steps, a.warmup)
+        print(json.dumps({"config": a.only_config, "steps": a.steps, "warmup": a.warmup, **res}), flush=True)
+        return
     headline_cfg = 3
     w = W.CONFIGS[headline_cfg]()
     log(f"[bench] headline: {w.name}")
