@@ -165,6 +165,7 @@ mvr::PagedAttentionPlan make_plan(const mvr_paged_attention_args* a, bool allow_
   plan.row_tiles = (int)((rows_max + tile_rows - 1) / tile_rows);
   const int max_chunks = (a->max_seq_len + mvr::kChunkTokens - 1) / mvr::kChunkTokens;
   const int64_t base_units = (int64_t)a->num_seqs * a->num_kv_heads * plan.row_tiles;
+  const bool ragged = a->sum_seq_lens > 0 && a->sum_seq_lens < (int64_t)a->max_seq_len * a->num_seqs;
   int cpp = chunks_per_partition_override();
   if (cpp <= 0) {
     // Split contexts so that the units fill the resident wavefront slots of
@@ -175,7 +176,6 @@ mvr::PagedAttentionPlan make_plan(const mvr_paged_attention_args* a, bool allow_
     if (slots <= 0) slots = 256 * 8; // no device to ask (sizing only)
     int64_t units_per_group = slots / ((int64_t)a->num_kv_heads * plan.row_tiles);
     if (units_per_group < 1) units_per_group = 1;
-    const bool ragged = a->sum_seq_lens > 0 && a->sum_seq_lens < (int64_t)a->max_seq_len * a->num_seqs;
     int64_t c;
     if (ragged) {
       // Ragged lengths (known through sum_seq_lens): each sequence's last
@@ -204,7 +204,14 @@ mvr::PagedAttentionPlan make_plan(const mvr_paged_attention_args* a, bool allow_
   if (cpp > max_chunks) cpp = max_chunks;
   plan.chunks_per_part = cpp;
   plan.max_parts = (max_chunks + cpp - 1) / cpp;
-  if (plan.max_parts > 1) {
+  // Block merge: a uniform batch split into exactly one block's worth of
+  // partitions (the batch-64 x 8K decode: 4 x 2048 tokens) puts the
+  // partitions of one (sequence, KV head, row tile) in one block and merges
+  // them in LDS, without partials in HBM or a merge launch; its blocks need
+  // no XCD padding.  MVR_ATTN_BLOCK_MERGE=false keeps the separate merge.
+  static const bool block_merge_enabled = env_bool("MVR_ATTN_BLOCK_MERGE", true);
+  plan.block_merge = block_merge_enabled && !ragged && plan.row_blocks == 1 && plan.max_parts == mvr::kWavesPerBlock;
+  if (plan.max_parts > 1 && !plan.block_merge) {
     // Pad so that one sequence's units fill a multiple of 8 blocks of 4
     // wavefronts: then (row tile, partition, KV head) maps to the same XCD
     // for every sequence (the padding units exit at once).
@@ -226,7 +233,7 @@ mvr::PagedAttentionPlan make_plan(const mvr_paged_attention_args* a, bool allow_
   }
   plan.num_units = base_units * plan.max_parts;
   plan.partial_bytes = 0;
-  if (plan.max_parts > 1) {
+  if (plan.max_parts > 1 && !plan.block_merge) {
     // [partial o][partial m, l]
     const size_t prow = (size_t)plan.num_units * tile_rows;
     plan.partial_bytes = align_up(prow * a->head_dim * sizeof(float), 256) + align_up(prow * 2 * sizeof(float), 256);

@@ -282,17 +282,30 @@ struct F32Traits {
 // ---------------------------------------------------------------------------
 // Occupancy floor (blocks per CU = wavefronts per SIMD) per dtype: the
 // largest that fits each variant without scratch.
-template <typename Tr, int D, int NB>
+//
+// BM (block merge): a block holds the kWavesPerBlock partitions of one
+// (sequence, KV head, row tile) instead of one partition of kWavesPerBlock
+// KV heads, and merges them through LDS at the end: no fp32 partials in HBM
+// and no merge launch.  The planner uses it when a uniform batch splits
+// every context into exactly kWavesPerBlock partitions (the wavefronts of a
+// block then do equal work); a partition without keys still takes part in
+// the block's barrier.
+template <typename Tr, int D, int NB, bool BM = false>
 __global__ __launch_bounds__(kWaveSize* kWavesPerBlock, Tr::template min_blocks<NB>()) void paged_attention_kernel(
     PagedAttentionParams p) {
   typedef typename Tr::elem T;
   constexpr int kTileRows = 16 * NB;
   __shared__ __attribute__((aligned(16))) T lds_all[kWavesPerBlock][kChunkTokens * D];
+  // BM: each wavefront's rows (O, m, l); rows padded by 4 floats so that the
+  // 16 rows of a float4 store fall in distinct banks.
+  constexpr int kMergeStride = D + 4;
+  __shared__ __attribute__((aligned(16))) float merge_o[BM ? kWavesPerBlock * kTileRows * kMergeStride : 4];
+  __shared__ float merge_ml[BM ? kWavesPerBlock * kTileRows * 2 : 2];
 
   const int l = lane_id();
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWaveSize);
   const int64_t unit = (int64_t)blockIdx.x * kWavesPerBlock + wave;
-  if (unit >= p.num_units) return;
+  if (!BM && unit >= p.num_units) return; // BM grids are exact: no wavefront may skip the block barrier
   T* lds = lds_all[wave];
 
   // KV head fastest: the wavefronts of one (sequence, partition) read the
@@ -303,13 +316,26 @@ __global__ __launch_bounds__(kWaveSize* kWavesPerBlock, Tr::template min_blocks<
   // shared by several sequences (a common prefix) hit in that XCD's L2.
   // (Dealing each XCD's blocks partition-major across sequences instead
   // measured slower: 142 vs 110 us on 16 sequences of 1K..16K tokens.)
-  int64_t rest = unit;
-  const int h = (int)(rest % p.num_kv_heads);
-  rest /= p.num_kv_heads;
-  const int part = (int)(rest % p.max_parts);
-  rest /= p.max_parts;
-  const int rt = (int)(rest % p.row_tiles);
-  const int b = (int)(rest / p.row_tiles);
+  // BM: block = (sequence, row tile, KV head) with the KV head fastest, so
+  // that with 8 KV heads block % 8 (its XCD) is the KV head for every
+  // sequence; wavefront = partition.
+  int h, part, rt, b;
+  if constexpr (BM) {
+    int64_t tile = blockIdx.x;
+    part = wave;
+    h = (int)(tile % p.num_kv_heads);
+    tile /= p.num_kv_heads;
+    rt = (int)(tile % p.row_tiles);
+    b = (int)(tile / p.row_tiles);
+  } else {
+    int64_t rest = unit;
+    h = (int)(rest % p.num_kv_heads);
+    rest /= p.num_kv_heads;
+    part = (int)(rest % p.max_parts);
+    rest /= p.max_parts;
+    rt = (int)(rest % p.row_tiles);
+    b = (int)(rest / p.row_tiles);
+  }
   // Partials are stored tile-major: slot = tile * max_parts + part.
   const int64_t slot = (((int64_t)b * p.num_kv_heads + h) * p.row_tiles + rt) * p.max_parts + part;
 
@@ -317,8 +343,8 @@ __global__ __launch_bounds__(kWaveSize* kWavesPerBlock, Tr::template min_blocks<
   const int rows = p.group_size * s.q_len;
   const int n_chunks = tile_chunks(s, p.group_size, rt, kTileRows);
   const int k0 = s.key_begin / kChunkTokens + part * p.chunks_per_part;
-  if (n_chunks == 0 || k0 >= n_chunks) return;
-  const int k1 = min(k0 + p.chunks_per_part, n_chunks);
+  if (!BM && (n_chunks == 0 || k0 >= n_chunks)) return;
+  const int k1 = min(k0 + p.chunks_per_part, n_chunks); // BM: k1 <= k0 for a partition without keys
   const int n_parts = tile_parts(s, n_chunks, p.chunks_per_part);
   const int g = l >> 4;
 
@@ -409,8 +435,10 @@ __global__ __launch_bounds__(kWaveSize* kWavesPerBlock, Tr::template min_blocks<
 
   typename Tr::kreg_t ka[Tr::kLoads], kb[Tr::kLoads];
   typename Tr::vreg_t va[Tr::kLoads], vb[Tr::kLoads];
-  load_chunk(k0, ka, va);
-  load_chunk(min(k0 + 1, k1 - 1), kb, vb);
+  if (k0 < k1) { // always, except a BM partition without keys (its chunks lie past the table)
+    load_chunk(k0, ka, va);
+    load_chunk(min(k0 + 1, k1 - 1), kb, vb);
+  }
   for (int k = k0; k < k1; k += 2) {
     process(k, ka, va);
     load_chunk(min(k + 2, k1 - 1), ka, va);
@@ -418,6 +446,78 @@ __global__ __launch_bounds__(kWaveSize* kWavesPerBlock, Tr::template min_blocks<
       process(k + 1, kb, vb);
       load_chunk(min(k + 3, k1 - 1), kb, vb);
     }
+  }
+
+  if constexpr (BM) {
+    // Every wavefront's rows into LDS (a partition without keys holds
+    // m = -inf, l = 0, O = 0 and lies past n_parts), then each wavefront
+    // merges rows wave, wave + 4, ... with the arithmetic of
+    // merge_partitions_kernel (same order, so the same bits).
+#pragma unroll
+    for (int nb = 0; nb < NB; nb++) {
+      const float ltot = wave_sum_across_groups(lsum[nb]);
+      const int rr = nb * 16 + (l & 15);
+      float* dst = merge_o + (wave * kTileRows + rr) * kMergeStride;
+#pragma unroll
+      for (int n = 0; n < D / 16; n++) *reinterpret_cast<float4v*>(dst + 16 * n + 4 * g) = o[nb][n];
+      if (g == 0) {
+        merge_ml[(wave * kTileRows + rr) * 2 + 0] = m[nb];
+        merge_ml[(wave * kTileRows + rr) * 2 + 1] = ltot;
+      }
+    }
+    __syncthreads();
+    static_assert(kWavesPerBlock == 4, "the den sum below follows a 4-partition butterfly");
+    constexpr int kPer = D / kWaveSize;
+    for (int rr = wave; rr < kTileRows; rr += kWavesPerBlock) {
+      const int rho = rt * kTileRows + rr;
+      if (rho >= rows || n_parts == 0) continue;
+      float mj[kWavesPerBlock], wl[kWavesPerBlock];
+      float mmax = -INFINITY;
+#pragma unroll
+      for (int j = 0; j < kWavesPerBlock; j++) {
+        mj[j] = j < n_parts ? merge_ml[(j * kTileRows + rr) * 2] : -INFINITY;
+        mmax = fmaxf(mmax, mj[j]);
+      }
+      const float m_use = mmax == -INFINITY ? 0.f : mmax;
+      float w[kWavesPerBlock];
+#pragma unroll
+      for (int j = 0; j < kWavesPerBlock; j++) {
+        w[j] = j < n_parts ? __builtin_amdgcn_exp2f(mj[j] - m_use) : 0.f;
+        wl[j] = j < n_parts ? w[j] * merge_ml[(j * kTileRows + rr) * 2 + 1] : 0.f;
+      }
+      // merge_partitions_kernel sums lane j's w_j l_j over the wavefront by
+      // xor-shuffles; with partitions in lanes 0..3 that is (0 + 2) + (1 + 3).
+      const float den = (wl[0] + wl[2]) + (wl[1] + wl[3]);
+      float acc[kPer];
+#pragma unroll
+      for (int e = 0; e < kPer; e++) acc[e] = 0.f;
+      for (int j = 0; j < n_parts; j++) {
+        const float* src = merge_o + (j * kTileRows + rr) * kMergeStride + l * kPer;
+#pragma unroll
+        for (int e = 0; e < kPer; e++) acc[e] = fmaf(w[j], src[e], acc[e]);
+      }
+      const int r = rho / s.q_len, i = rho % s.q_len;
+      const float inv = 1.f / den;
+      const int64_t srow = (int64_t)(h * p.group_size + r) * p.state_tokens + s.q_start + i;
+      if (p.state_o) {
+#pragma unroll
+        for (int e = 0; e < kPer; e++) p.state_o[srow * D + l * kPer + e] = acc[e] * inv;
+        if (l == 0) p.state_lse[srow] = m_use + __log2f(den);
+        continue;
+      }
+      T* out = static_cast<T*>(p.out) + (int64_t)(h * p.group_size + r) * p.out_stride_head +
+               (int64_t)(s.q_start + i) * p.out_stride_token + l * kPer;
+      const PrefixWeights pw = prefix_weights(p, b, srow, m_use + __log2f(den));
+      if (pw.has) {
+        const float* src = p.prefix_o + srow * D + l * kPer;
+#pragma unroll
+        for (int e = 0; e < kPer; e++) out[e] = (T)((pw.wa * src[e] + pw.wb * (acc[e] * inv)) * pw.inv);
+      } else {
+#pragma unroll
+        for (int e = 0; e < kPer; e++) out[e] = (T)(acc[e] * inv);
+      }
+    }
+    return;
   }
 
 #pragma unroll
@@ -563,6 +663,18 @@ __global__ __launch_bounds__(256) void merge_partitions_kernel(PagedAttentionPar
 template <typename Tr, int D, int NB>
 hipError_t launch_typed(const PagedAttentionPlan& plan, const PagedAttentionParams& params, hipStream_t stream) {
   const int64_t blocks = (plan.num_units + kWavesPerBlock - 1) / kWavesPerBlock;
+  if constexpr (NB == 1) {
+    if (plan.block_merge) {
+      // One block per (sequence, KV head, row tile): exactly num_units / 4 blocks.
+      if (plan.max_parts != kWavesPerBlock ||
+          plan.num_units != (int64_t)params.num_seqs * params.num_kv_heads * params.row_tiles * kWavesPerBlock)
+        return hipErrorInvalidValue;
+      hipLaunchKernelGGL((paged_attention_kernel<Tr, D, NB, true>), dim3((unsigned)blocks),
+                         dim3(kWaveSize * kWavesPerBlock), 0, stream, params);
+      return hipGetLastError();
+    }
+  }
+  if (plan.block_merge) return hipErrorInvalidValue; // planned for one 16-row block only
   hipLaunchKernelGGL((paged_attention_kernel<Tr, D, NB>), dim3((unsigned)blocks), dim3(kWaveSize * kWavesPerBlock), 0,
                      stream, params);
   hipError_t err = hipGetLastError();

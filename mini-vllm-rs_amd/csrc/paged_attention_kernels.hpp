@@ -63,6 +63,7 @@ struct PagedAttentionPlan {
   size_t partial_bytes; // workspace for partials (0 when max_parts == 1)
   bool prefill;         // chunked-prefill kernel (paged_prefill.hip) instead of the split-context one
   int kv_splits;        // prefill: key-range splits per 128-row tile
+  bool block_merge;     // max_parts == kWavesPerBlock: one block per tile, partitions merged in LDS
 };
 
 hipError_t launch_paged_attention(const PagedAttentionPlan& plan, PagedAttentionParams params, hipStream_t stream);

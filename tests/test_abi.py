@@ -97,6 +97,15 @@ def test_workspace_too_small_is_rejected():
     assert rc == M.MVR_E_WORKSPACE and "smaller than" in err
 
 
+def test_block_merge_plan_needs_no_workspace():
+    # The batch-64 x 8K decode splits every context into one block's worth of partitions (4): they merge in
+    # LDS, so the call needs no workspace.  A ragged length hint plans the separate merge again.
+    uniform = _args(num_seqs=64, max_seq_len=8192, max_pages_per_seq=512, sum_seq_lens=64 * 8192)
+    assert M.workspace_size(uniform) == 0
+    ragged = _args(num_seqs=64, max_seq_len=8192, max_pages_per_seq=512, sum_seq_lens=64 * 8192 - 4096)
+    assert M.workspace_size(ragged) > 0
+
+
 def test_validate_mirrors_reference_errors():
     a = _args()
     bt = [[i for i in range(64)], [64 + i for i in range(64)]]
