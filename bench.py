@@ -292,9 +292,10 @@ def main():
             "unit": "GB/s",
             "frac": round(value / HBM_PEAK_GBS, 4),
             "traffic": traffic,
-            "timed": "mean duration of the whole attention call (paged_attention_kernel + merge_partitions_kernel) "
-                     "between HIP events recorded on the launch stream; the rocprofv3 kernel-trace summary in "
-                     "profiles/ lists both kernels' averages, whose sum this mean should match",
+            "timed": "mean duration of the whole attention call between HIP events recorded on the launch stream "
+                     "(one launch of paged_attention_kernel, whose 4 context partitions per (sequence, KV head) "
+                     "merge in LDS); the rocprofv3 kernel-trace summary in profiles/ lists its average, which "
+                     "this mean should match",
         },
     }
     if not a.only_headline:
