@@ -8,9 +8,15 @@ call needs no workspace.  Same bar as every call: 2e-3 (F16) / 1e-5 (F32)
 against the oracle.  Covers F16 at head_dim 128 (the batch-64 decode shape at
 1K tokens), ragged lengths planned as uniform (no length hint), so that short
 sequences leave partitions without keys that still join the block's merge,
-and F32 at head_dim 64.
+and F32 at head_dim 64.  The block-merge launch is also compared bit for bit
+with the two-launch plan (fp32 partials in the workspace, merge kernel) on the
+same batch, computed in a child process with MVR_ATTN_BLOCK_MERGE=false (the
+flag is read once per process): both merge the same four partition states
+with the same weights in the same order.
 """
 import math
+import os
+import subprocess
 import sys
 
 import numpy as np
@@ -87,3 +93,54 @@ def test_ragged_lengths_planned_uniform():
 
 def test_uniform_f32_d64():
     run_and_check(decode_workload("f32 D64 256 x 512", "f32", 14, 2, 64, [512] * 256, 63), hint=True)
+
+
+def _uniform_f16_workload():
+    return decode_workload("f16 D128 64 x 1024", "f16", 32, 8, 128, [1024] * 64, 61)
+
+
+def _attend(w):
+    t = W.device_tensors(w, W.host_values(w))
+    args = M.make_args(t["q"], t["key_pool"], t["value_pool"], t["block_tables"], t["seq_lens"], t["cu_q_lens"],
+                       t["q"], max_q_len=w.max_q_len, max_seq_len=w.max_seq_len, sum_seq_lens=int(w.seq_lens.sum()))
+    need = M.workspace_size(args)
+    out = M.paged_attention(t["q"], t["key_pool"], t["value_pool"], t["block_tables"], t["seq_lens"], t["cu_q_lens"],
+                            max_q_len=w.max_q_len, max_seq_len=w.max_seq_len, sum_seq_lens=int(w.seq_lens.sum()))
+    torch.cuda.synchronize()
+    return out.cpu().numpy(), need
+
+
+def _two_launch_child(path):
+    """Child-process side: the same batch with block merge switched off."""
+    M.load_library()
+    out, need = _attend(_uniform_f16_workload())
+    assert need > 0, "expected the two-launch plan (fp32 partials in the workspace)"
+    np.save(path, out)
+
+
+_CHILD = (
+    "import sys\n"
+    "sys.path[:0] = sys.argv[2].split('|')\n"
+    "import test_gpu_block_merge as T\n"
+    "T._two_launch_child(sys.argv[1])\n"
+    "print('two-launch plan done', flush=True)\n"
+)
+
+
+def test_bit_identical_to_two_launch_plan(tmp_path):
+    w = _uniform_f16_workload()
+    got, need = _attend(w)
+    assert need == 0, "expected the block-merge plan (no workspace)"
+    here = os.path.dirname(os.path.abspath(__file__))
+    root = os.path.dirname(here)
+    paths = "|".join([here, root, os.path.join(root, "oracle"), os.path.join(root, "mini-vllm-rs_amd")])
+    dst = str(tmp_path / "two_launch.npy")
+    say("[block-merge] two-launch plan in a child process (MVR_ATTN_BLOCK_MERGE=false)")
+    child = subprocess.run([sys.executable, "-c", _CHILD, dst, paths], env=dict(os.environ, MVR_ATTN_BLOCK_MERGE="false"),
+                           capture_output=True, text=True, timeout=180)
+    assert child.returncode == 0, child.stdout[-2000:] + child.stderr[-2000:]
+    two = np.load(dst)
+    assert got.dtype == np.float16 and two.dtype == np.float16 and got.shape == two.shape
+    diff = int(np.count_nonzero(got.view(np.uint16) != two.view(np.uint16)))
+    say(f"[block-merge] {w.name}: {diff} of {got.size} outputs differ from the two-launch plan")
+    assert diff == 0
