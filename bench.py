@@ -98,10 +98,26 @@ def cpu_baseline(W):
             break
     per_call = el / reps
     gbs = sample.algorithmic_bytes() / per_call / 1e9
+    # The same dataflow on one thread, on one sequence (all 8 kv heads, 8192 tokens), for about 5 s.
+    one = W.llama3_8b_decode_b64_8k_f16(batch=1)
+    q1, k1, v1 = W.host_values(one)
+    reps1 = 0
+    t0 = time.perf_counter()
+    while True:
+        oracle.paged_attention(q1, k1, v1, one.block_tables, one.seq_lens, one.cu_q_lens, one.num_q_heads,
+                               one.num_kv_heads, one.head_dim, one.page_size, dtype=oracle.F16, num_threads=1)
+        reps1 += 1
+        el1 = time.perf_counter() - t0
+        if el1 > 5.0:
+            break
+    per_call1 = el1 / reps1
     return dict(value=round(gbs, 3), unit="GB/s", cores=threads, kind="port",
                 sample=f"{sample.num_seqs} of {full.num_seqs} sequences x 8 kv heads x 8192 tokens (F16 reference dataflow, "
                        f"{reps} calls, {per_call * 1e3:.1f} ms/call; full batch extrapolates to "
                        f"{per_call * full.num_seqs / sample.num_seqs * 1e3:.0f} ms/step)",
+                single_thread=dict(value=round(one.algorithmic_bytes() / per_call1 / 1e9, 3), unit="GB/s", cores=1,
+                                   sample=f"1 of {full.num_seqs} sequences x 8 kv heads x 8192 tokens, {reps1} calls, "
+                                          f"{per_call1 * 1e3:.1f} ms/call"),
                 host=platform.processor() or platform.machine())
 
 
