@@ -195,8 +195,10 @@ class CascadeRunner(Runner):
             raise self.M.MvrError(rc, self.lib.mvr_last_error().decode())
 
 
-def measure_cascade(W, M, torch, cfg, steps, warmup):
-    w = W.CONFIGS[cfg]()
+def measure_cascade(W, M, torch, cfg, steps, warmup, with_plain=False):
+    """cfg: a key of W.CONFIGS or a workload builder.  with_plain: also time the plain call on the same
+    tensors, for the speedup."""
+    w = W.CONFIGS[cfg]() if isinstance(cfg, int) else cfg()
     t = W.device_tensors(w, None)
     r = CascadeRunner(w, t, torch, M, W)
     wall, per = time_steps(r, torch, steps, warmup)
@@ -205,6 +207,14 @@ def measure_cascade(W, M, torch, cfg, steps, warmup):
     res = dict(workload=f"{w.name} through cascade attention ({len(w.prefix_groups)} prefix groups)",
                us_per_step_median=round(med, 2), unique_bytes=ub, unique_gbs=round(ub / (med * 1e-6) / 1e9, 1),
                hbm_frac=round(ub / (med * 1e-6) / 1e9 / HBM_PEAK_GBS, 4))
+    if with_plain:
+        del r
+        p = Runner(w, t, torch, M)
+        _, per_p = time_steps(p, torch, steps, warmup)
+        med_p = per_p[len(per_p) // 2]
+        res.update(plain_us_per_step_median=round(med_p, 2), speedup_vs_plain=round(med_p / med, 3),
+                   logical_bytes=w.algorithmic_bytes())
+        r = p
     del t, r
     torch.cuda.empty_cache()
     return res
@@ -322,6 +332,9 @@ def main():
         result["configs"] = per_cfg
         log("[bench] config 5 through cascade attention")
         result["cascade"] = {"5": measure_cascade(W, M, torch, 5, max(20, a.steps // 2), a.warmup)}
+        log("[bench] shared-prompt decode, cascade and plain")
+        result["cascade"]["shared_prompt"] = measure_cascade(W, M, torch, W.llama3_8b_shared_prompt_decode_f16,
+                                                             max(20, a.steps // 2), a.warmup, with_plain=True)
         result["rope_append"] = {}
         for cfg in (3, 4):
             log(f"[bench] rope+append, config {cfg}")

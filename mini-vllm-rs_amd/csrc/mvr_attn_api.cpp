@@ -211,7 +211,33 @@ mvr::PagedAttentionPlan make_plan(const mvr_paged_attention_args* a, bool allow_
   // no XCD padding.  MVR_ATTN_BLOCK_MERGE=false keeps the separate merge.
   static const bool block_merge_enabled = env_bool("MVR_ATTN_BLOCK_MERGE", true);
   plan.block_merge = block_merge_enabled && !ragged && plan.row_blocks == 1 && plan.max_parts == mvr::kWavesPerBlock;
-  if (plan.max_parts > 1 && !plan.block_merge) {
+  // Dense layout for ragged batches with one row tile (dense_unit in
+  // paged_attention.hip): the live units are numbered from 0, so in-order
+  // dispatch balances them over the CUs and XCDs, where slot == partition
+  // leaves a ragged batch's live early partitions piled onto some XCDs (64
+  // sequences of 256..2048 tokens: 1.5x the mean load on two XCDs; rotating
+  // each sequence's partitions instead left units starting up to 29 us late).
+  // But slot == partition also keeps partition p of every sequence on one XCD,
+  // so pages shared by several sequences (a common prefix) are read from HBM
+  // once per XCD, and it suits few or long sequences: measured, the dense
+  // layout took 64 ragged sequences from 79 to 72 us and the cascade suffix
+  // pass of 64 sequences behind an 8K-token prompt from 119 to 110 us, but the
+  // plain call on that shared prompt from 242 to 280 us, the 16-sequence
+  // verify workload from 110 to 115 us (its cascade suffix pass from 127 to
+  // 130) and 8 Qwen2-0.5B sequences from 14.2 to 15.0 us.  It is taken when
+  // the batch has many sequences and most of the slot == partition grid
+  // would hold no work (estimated from the length hint), which selects the
+  // two winning cases and none of the others.  MVR_ATTN_DENSE_RAGGED=false
+  // turns it off.
+  static const bool dense_enabled = env_bool("MVR_ATTN_DENSE_RAGGED", true);
+  bool dense = false;
+  if (dense_enabled && ragged && plan.row_tiles == 1 && plan.max_parts > 1 && !plan.block_merge && a->num_seqs >= 32) {
+    const int64_t chunk_tokens = (int64_t)mvr::kChunkTokens * plan.chunks_per_part;
+    const int64_t est_live = (a->sum_seq_lens + chunk_tokens - 1) / chunk_tokens + a->num_seqs / 2;
+    dense = est_live * 10 < (int64_t)a->num_seqs * plan.max_parts * 7; // live fraction < 0.7
+  }
+  plan.dense_parts = dense;
+  if (plan.max_parts > 1 && !plan.block_merge && !plan.dense_parts) {
     // Pad so that one sequence's units fill a multiple of 8 blocks of 4
     // wavefronts: then (row tile, partition, KV head) maps to the same XCD
     // for every sequence (the padding units exit at once).

@@ -102,6 +102,72 @@ __device__ __forceinline__ int tile_parts(const SeqInfo& s, int n_chunks, int ch
   return n_chunks > kb ? (n_chunks - kb + chunks_per_part - 1) / chunks_per_part : 0;
 }
 
+// Inclusive prefix sum over the 64 lanes of a wavefront.
+__device__ __forceinline__ int wave_inclusive_sum(int v) {
+  const int l = lane_id();
+#pragma unroll
+  for (int off = 1; off < kWaveSize; off <<= 1) {
+    const int t = __shfl_up(v, off);
+    if (l >= off) v += t;
+  }
+  return v;
+}
+
+// Dense layout of a ragged batch (one row tile per sequence and KV head):
+// the live (sequence, partition) pairs are numbered from 0, 64 sequences at
+// a time: first those sequences' full partitions (chunks_per_part chunks
+// each), sequence by sequence, then each one's last, possibly partial,
+// partition.  Work index w maps to (b, part); false once w is past every live
+// pair.  Each wavefront derives its pair from the sequence lengths with one
+// wave-wide scan per 64 sequences, so the grid needs no per-call table: it
+// is sized for the worst case (max_parts per sequence) and its tail exits at
+// once.  In-order dispatch then hands out the live units like a work queue,
+// longest first within each 64 sequences, spread over all XCDs.
+__device__ __forceinline__ SeqInfo lane_seq(const SeqInfo& s, int src) {
+  return SeqInfo{__shfl(s.seq_len, src), __shfl(s.q_start, src), __shfl(s.q_len, src), __shfl(s.key_begin, src),
+                 __shfl(s.key_end, src)};
+}
+
+// Also returns the sequence's SeqInfo (loaded by one lane of the scan), so the
+// unit starts without a second round trip for it.
+__device__ bool dense_unit(const PagedAttentionParams& p, int64_t w, int tile_rows, int& b_out, int& part_out,
+                           SeqInfo& s_out) {
+  const int l = lane_id();
+  int64_t base = 0;
+  for (int b0 = 0; b0 < p.num_seqs; b0 += kWaveSize) {
+    const int b = b0 + l;
+    int n = 0;
+    SeqInfo s{0, 0, 0, 0, 0};
+    if (b < p.num_seqs) {
+      s = load_seq(p, b);
+      n = tile_parts(s, tile_chunks(s, p.group_size, 0, tile_rows), p.chunks_per_part);
+    }
+    const int full = n > 0 ? n - 1 : 0, last = n > 0 ? 1 : 0;
+    const int full_incl = wave_inclusive_sum(full), last_incl = wave_inclusive_sum(last);
+    const int full_total = __shfl(full_incl, kWaveSize - 1), last_total = __shfl(last_incl, kWaveSize - 1);
+    if (w < base + full_total) {
+      const int64_t r = w - base;
+      const uint64_t hit = __ballot(r >= full_incl - full && r < full_incl);
+      const int src = __builtin_ctzll(hit);
+      b_out = b0 + src;
+      part_out = (int)(r - __shfl(full_incl - full, src));
+      s_out = lane_seq(s, src);
+      return true;
+    }
+    if (w < base + full_total + last_total) {
+      const int64_t r = w - base - full_total;
+      const uint64_t hit = __ballot(last == 1 && r == last_incl - 1);
+      const int src = __builtin_ctzll(hit);
+      b_out = b0 + src;
+      part_out = __shfl(n, src) - 1;
+      s_out = lane_seq(s, src);
+      return true;
+    }
+    base += full_total + last_total;
+  }
+  return false;
+}
+
 // Cascade suffix pass: weights that merge this pass's normalised row (log2
 // sum lb) with the prefix pass's state of the same row (srow):
 //   out = (wa * o_a + wb * o_b) * inv.
@@ -290,7 +356,9 @@ struct F32Traits {
 // every context into exactly kWavesPerBlock partitions (the wavefronts of a
 // block then do equal work); a partition without keys still takes part in
 // the block's barrier.
-template <typename Tr, int D, int NB, bool BM = false>
+// DENSE: the dense layout of a ragged batch (dense_unit); a separate instantiation,
+// so that the slot == partition kernels compile exactly as without it.
+template <typename Tr, int D, int NB, bool BM = false, bool DENSE = false>
 __global__ __launch_bounds__(kWaveSize* kWavesPerBlock, Tr::template min_blocks<NB>()) void paged_attention_kernel(
     PagedAttentionParams p) {
   typedef typename Tr::elem T;
@@ -320,6 +388,7 @@ __global__ __launch_bounds__(kWaveSize* kWavesPerBlock, Tr::template min_blocks<
   // that with 8 KV heads block % 8 (its XCD) is the KV head for every
   // sequence; wavefront = partition.
   int h, part, rt, b;
+  SeqInfo s;
   if constexpr (BM) {
     int64_t tile = blockIdx.x;
     part = wave;
@@ -327,6 +396,12 @@ __global__ __launch_bounds__(kWaveSize* kWavesPerBlock, Tr::template min_blocks<
     tile /= p.num_kv_heads;
     rt = (int)(tile % p.row_tiles);
     b = (int)(tile / p.row_tiles);
+  } else if constexpr (DENSE) {
+    h = (int)(unit % p.num_kv_heads);
+    rt = 0;
+    // part >= max_parts only if a seq_len exceeds max_seq_len (a broken
+    // contract): its partial slot would lie in the next tile, so drop it.
+    if (!dense_unit(p, unit / p.num_kv_heads, kTileRows, b, part, s) || part >= p.max_parts) return;
   } else {
     int64_t rest = unit;
     h = (int)(rest % p.num_kv_heads);
@@ -339,7 +414,7 @@ __global__ __launch_bounds__(kWaveSize* kWavesPerBlock, Tr::template min_blocks<
   // Partials are stored tile-major: slot = tile * max_parts + part.
   const int64_t slot = (((int64_t)b * p.num_kv_heads + h) * p.row_tiles + rt) * p.max_parts + part;
 
-  const SeqInfo s = load_seq(p, b);
+  if constexpr (BM || !DENSE) s = load_seq(p, b);
   const int rows = p.group_size * s.q_len;
   const int n_chunks = tile_chunks(s, p.group_size, rt, kTileRows);
   const int k0 = s.key_begin / kChunkTokens + part * p.chunks_per_part;
@@ -591,7 +666,8 @@ __global__ __launch_bounds__(256) void merge_partitions_kernel(PagedAttentionPar
   const int rho = rt * kTileRows + lr;
   if (rho >= p.group_size * s.q_len) return;
   const int n_chunks = tile_chunks(s, p.group_size, rt, kTileRows);
-  const int n_parts = tile_parts(s, n_chunks, p.chunks_per_part);
+  // At most max_parts partials exist per tile (more only if a seq_len exceeds max_seq_len).
+  const int n_parts = min(tile_parts(s, n_chunks, p.chunks_per_part), p.max_parts);
   if (n_parts <= 1) return;
 
   // Partial row of partition j: (tile * max_parts + j) * kTileRows + lr.
@@ -675,8 +751,14 @@ hipError_t launch_typed(const PagedAttentionPlan& plan, const PagedAttentionPara
     }
   }
   if (plan.block_merge) return hipErrorInvalidValue; // planned for one 16-row block only
-  hipLaunchKernelGGL((paged_attention_kernel<Tr, D, NB>), dim3((unsigned)blocks), dim3(kWaveSize * kWavesPerBlock), 0,
-                     stream, params);
+  if (plan.dense_parts) {
+    if (params.row_tiles != 1) return hipErrorInvalidValue; // dense_unit walks row tile 0 only
+    hipLaunchKernelGGL((paged_attention_kernel<Tr, D, NB, false, true>), dim3((unsigned)blocks),
+                       dim3(kWaveSize * kWavesPerBlock), 0, stream, params);
+  } else {
+    hipLaunchKernelGGL((paged_attention_kernel<Tr, D, NB>), dim3((unsigned)blocks), dim3(kWaveSize * kWavesPerBlock),
+                       0, stream, params);
+  }
   hipError_t err = hipGetLastError();
   if (err != hipSuccess || plan.max_parts <= 1) return err;
   const int64_t tiles = (int64_t)params.num_seqs * params.num_kv_heads * params.row_tiles;

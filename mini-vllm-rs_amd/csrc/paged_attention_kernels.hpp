@@ -64,6 +64,7 @@ struct PagedAttentionPlan {
   bool prefill;         // chunked-prefill kernel (paged_prefill.hip) instead of the split-context one
   int kv_splits;        // prefill: key-range splits per 128-row tile
   bool block_merge;     // max_parts == kWavesPerBlock: one block per tile, partitions merged in LDS
+  bool dense_parts;     // ragged split plan: live units first, in a dense order (see dense_unit)
 };
 
 hipError_t launch_paged_attention(const PagedAttentionPlan& plan, PagedAttentionParams params, hipStream_t stream);

@@ -2,7 +2,8 @@
 
 Five shapes: Qwen2-0.5B decode (F32 and batched F16), Llama-3-8B batch-64 x 8K
 decode, Qwen2-7B chunked prefill and Llama-3-8B speculative verification with
-shared prefix pages.  Block tables, lengths and values are derived from a seed
+shared prefix pages; and a sixth for cascade attention, a Llama-3-8B decode
+batch whose sequences share one long prompt prefix.  Block tables, lengths and values are derived from a seed
 so the GPU and the CPU see identical bytes: tables and lengths with numpy's
 PCG64, values either with numpy (host, for parity tests) or torch's device
 generator (fast, for benchmarks).
@@ -181,6 +182,30 @@ def llama3_8b_spec_verify_f16() -> Workload:
     return Workload("llama3-8b spec-verify f16 b16 q5 ctxU[1024,16384] shared-prefix", "f16", 32, 8, 128, 16,
                     num_pages, 0.3, seq_lens, np.full(16, q, np.int32), bt, seed, shared_pages=12 * shared,
                     prefix_groups=[(4 * g, 4, 1024) for g in range(4)])
+
+
+def llama3_8b_shared_prompt_decode_f16(batch: int = 64, prompt: int = 8192, lo: int = 256, hi: int = 2048) -> Workload:
+    """One decode step of `batch` sequences that share a `prompt`-token prefix (a system prompt: one set of
+    physical pages, as find_longest_cached_prefix hands a cached prefix's pages to every request that
+    matches it, prefix_index.rs:174-211) followed by private contexts of U[lo, hi] tokens."""
+    seed = SEED_BASE + 6
+    rng = np.random.default_rng(seed)
+    q = 1
+    seq_lens = (prompt + rng.integers(lo, hi, size=batch, endpoint=True) + q).astype(np.int32)
+    shared = prompt // 16
+    private = [math.ceil(int(L) / 16) - shared for L in seq_lens]
+    num_pages = shared + sum(private)
+    perm = rng.permutation(num_pages).astype(np.int32)
+    bt = np.zeros((batch, max(p + shared for p in private)), np.int32)
+    bt[:, :shared] = perm[:shared]
+    used = shared
+    for s in range(batch):
+        bt[s, shared:shared + private[s]] = perm[used:used + private[s]]
+        used += private[s]
+    # The prompt's pages are read by every sequence; batch - 1 of those reads are repeats.
+    return Workload(f"llama3-8b decode f16 b{batch} shared-prompt {prompt} + ctxU[{lo},{hi}]", "f16", 32, 8, 128, 16,
+                    num_pages, 0.3, seq_lens, np.full(batch, q, np.int32), bt, seed,
+                    shared_pages=(batch - 1) * shared, prefix_groups=[(0, batch, prompt)])
 
 
 CONFIGS = {

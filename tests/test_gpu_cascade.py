@@ -7,7 +7,8 @@ plain call's: 2e-3 (F16) / 1e-5 (F32) against the oracle, which knows nothing
 of the groups.  Covers the speculative-verification workload's own groups (4 x
 4 sequences sharing 1024 tokens), ragged groups with a lone sequence and a
 group of one, a prefix pass that takes the chunked-prefill kernel (many rows
-per group), F32 and head_dim 64, and a call with no group at all.
+per group), F32 and head_dim 64, a call with no group at all, and a decode
+batch of 64 sequences sharing one 8192-token prompt (plain call checked too).
 """
 import math
 import sys
@@ -83,6 +84,22 @@ def test_spec_verify_groups_match_oracle():
     groups = [(4 * g, 4, 1024) for g in range(4)]
     got = run_cascade(w, t, groups, [1024] * 16)
     check(w, vals, got, "spec-verify, 4 groups x 4 sequences, 1024-token prefixes")
+
+
+def test_shared_prompt_decode_matches_oracle():
+    # 64 decode sequences share one 8192-token prompt (a single group of 64: 256 grouped rows, so the prefix
+    # pass takes the chunked-prefill kernel), then private contexts of 256..2048 tokens; the plain call on
+    # the same tensors is checked too.
+    w = W.llama3_8b_shared_prompt_decode_f16()
+    vals = W.host_values(w)
+    t = W.device_tensors(w, vals)
+    got = run_cascade(w, t, [(0, w.num_seqs, 8192)], [8192] * w.num_seqs)
+    check(w, vals, got, "shared prompt, 64 sequences x 8192-token prefix")
+    plain = M.paged_attention(t["q"], t["key_pool"], t["value_pool"], t["block_tables"], t["seq_lens"],
+                              t["cu_q_lens"], max_q_len=w.max_q_len, max_seq_len=w.max_seq_len,
+                              sum_seq_lens=int(w.seq_lens.sum()))
+    torch.cuda.synchronize()
+    check(w, vals, plain.float().cpu().numpy(), "shared prompt, plain call")
 
 
 def shared_prefix_workload(dtype, d, page_size, q_lens, cached, groups, hq=8, hkv=2, seed=3):
