@@ -417,10 +417,19 @@ __global__ __launch_bounds__(kWaveSize* kWavesPerBlock, Tr::template min_blocks<
   if constexpr (BM || !DENSE) s = load_seq(p, b);
   const int rows = p.group_size * s.q_len;
   const int n_chunks = tile_chunks(s, p.group_size, rt, kTileRows);
-  const int k0 = s.key_begin / kChunkTokens + part * p.chunks_per_part;
-  if (!BM && (n_chunks == 0 || k0 >= n_chunks)) return;
-  const int k1 = min(k0 + p.chunks_per_part, n_chunks); // BM: k1 <= k0 for a partition without keys
+  // The tile's n_parts partitions split its chunks evenly (their lengths differ
+  // by at most one chunk and lie in (chunks_per_part / 2, chunks_per_part]
+  // when n_parts > 1), instead of n_parts - 1 full partitions and a short
+  // remainder: in a ragged batch the full-length units set the critical path
+  // while the remainders finish early.  A uniform batch whose context is a
+  // multiple of chunks_per_part gets the same boundaries either way.
   const int n_parts = tile_parts(s, n_chunks, p.chunks_per_part);
+  const int kb0 = s.key_begin / kChunkTokens;
+  const int64_t span = n_chunks > kb0 ? n_chunks - kb0 : 0;
+  const int k0 = n_parts > 0 ? kb0 + (int)((int64_t)part * span / n_parts) : kb0;
+  if (!BM && (n_chunks == 0 || k0 >= n_chunks)) return;
+  // BM: k1 <= k0 for a partition without keys (part >= n_parts)
+  const int k1 = n_parts > 0 ? min(kb0 + (int)((int64_t)(part + 1) * span / n_parts), n_chunks) : kb0;
   const int g = l >> 4;
 
   // Query rows of this lane (one per row block) and their causal limits.
