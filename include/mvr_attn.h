@@ -71,7 +71,8 @@ typedef struct mvr_paged_attention_args {
   int32_t num_q_heads;
   int32_t num_kv_heads;      /* divides num_q_heads */
   int32_t head_dim;          /* 64 or 128 */
-  int32_t page_size;         /* per_page_token_count; a multiple of 16 */
+  int32_t page_size;         /* per_page_token_count, any positive value; a size that is not a multiple
+                                of 16 is repacked into 16-token pages in the workspace first */
   int64_t num_pages;         /* page_count of each pool */
   int32_t max_pages_per_seq; /* row stride of block_tables */
   int32_t max_q_len;         /* >= every q_len (host-side bound, sizes the grid) */
@@ -96,9 +97,12 @@ typedef struct mvr_paged_attention_args {
 
 /* Bytes of workspace mvr_paged_attention needs for these arguments (depends
    only on the scalar fields; 0 when no sequence is split into context
-   partitions).  The workspace holds fp32 partial results of the partitions;
-   its contents need no initialisation and are dead after the call.  Calls
-   that share a workspace must not overlap in time. */
+   partitions and page_size is a multiple of 16).  The workspace holds fp32
+   partial results of the partitions and, when page_size is not a multiple of
+   16, a copy of the batch's K/V in 16-token pages (num_seqs x
+   ceil(max_seq_len / 16) pages) with its block table; its contents need no
+   initialisation and are dead after the call.  Calls that share a workspace
+   must not overlap in time. */
 size_t mvr_paged_attention_workspace_size(const mvr_paged_attention_args* args);
 
 /* Batched page-wise attention (decode, speculative verification and chunked
@@ -135,7 +139,8 @@ typedef struct mvr_cascade_groups {
   int32_t max_prefix_len;            /* >= every group's prefix tokens */
   const int32_t* group_cu_q_lens;    /* device [num_groups + 1]: packed-token range of each group's members */
   const int32_t* group_prefix_lens;  /* device [num_groups]: shared tokens, a multiple of page_size (0 allowed)
-                                        and <= every member's cached_kv_len */
+                                        and <= every member's cached_kv_len; cascade calls need a page_size
+                                        that is a multiple of 16 */
   const int32_t* group_block_tables; /* device [num_groups, max_pages_per_seq]: the shared pages */
   const int32_t* seq_prefix_lens;    /* device [num_seqs]: prefix tokens of the sequence's group, 0 if none */
   int64_t sum_prefix_lens;           /* optional planning hint: sum of seq_prefix_lens (0 = unknown) */

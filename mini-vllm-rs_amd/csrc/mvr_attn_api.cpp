@@ -90,9 +90,7 @@ int check_scalars(const mvr_paged_attention_args* a) {
                 a->num_kv_heads);
   if (a->head_dim != 64 && a->head_dim != 128)
     return fail(MVR_E_UNSUPPORTED, "head_dim %d is not supported (64 or 128)", a->head_dim);
-  if (a->page_size < mvr::kChunkTokens || a->page_size % mvr::kChunkTokens != 0)
-    return fail(MVR_E_UNSUPPORTED, "page_size %d is not a positive multiple of %d", a->page_size,
-                mvr::kChunkTokens);
+  if (a->page_size < 1) return fail(MVR_E_INVALID_ARGUMENT, "page_size must be positive");
   if (a->num_pages < 1) return fail(MVR_E_INVALID_ARGUMENT, "num_pages must be positive");
   if (a->max_q_len < 1) return fail(MVR_E_INVALID_ARGUMENT, "each forward input must contain at least one token");
   if (a->sum_seq_lens < 0 || (a->sum_seq_lens > 0 && a->sum_seq_lens > (int64_t)a->max_seq_len * a->num_seqs))
@@ -381,6 +379,41 @@ int check_workspace(const mvr_paged_attention_args* a, size_t need) {
   return MVR_OK;
 }
 
+// Page sizes that are not a multiple of 16 (the reference allows any
+// per_page_token_count; its own tests use 2 and 3): the kernels read whole
+// 16-token chunks of one page, so such a call first repacks every sequence's
+// tokens into 16-token pages in the workspace (launch_repack_pages: pages16
+// pages per sequence at fixed stride, plus their block table), then runs the
+// plan of that layout.  The attention is the same (only where the keys live
+// changes), at the cost of one more copy of the K/V the batch reads.
+// Workspace: [keys][values][block table][the plan's partials].
+struct RepackPlan {
+  mvr_paged_attention_args a16; // the call on the repacked layout (pointers into the workspace)
+  mvr::PagedAttentionPlan plan;
+  int pages16;
+  size_t off_part, total;
+};
+
+RepackPlan make_repack_plan(const mvr_paged_attention_args* a, char* ws) {
+  RepackPlan r;
+  r.pages16 = (a->max_seq_len + mvr::kChunkTokens - 1) / mvr::kChunkTokens;
+  const int es = a->dtype == MVR_DTYPE_F16 ? 2 : 4;
+  const size_t pool = (size_t)a->num_seqs * r.pages16 * a->num_kv_heads * mvr::kChunkTokens * a->head_dim * es;
+  const size_t table = (size_t)a->num_seqs * r.pages16 * sizeof(int32_t);
+  const size_t off_v = align_up(pool, 256), off_bt = off_v + align_up(pool, 256);
+  r.off_part = off_bt + align_up(table, 256);
+  r.a16 = *a;
+  r.a16.page_size = mvr::kChunkTokens;
+  r.a16.num_pages = (int64_t)a->num_seqs * r.pages16;
+  r.a16.max_pages_per_seq = r.pages16;
+  r.a16.key_pool = ws;
+  r.a16.value_pool = ws ? ws + off_v : nullptr;
+  r.a16.block_tables = ws ? reinterpret_cast<const int32_t*>(ws + off_bt) : nullptr;
+  r.plan = make_plan(&r.a16);
+  r.total = r.off_part + r.plan.partial_bytes;
+  return r;
+}
+
 // Cascade attention: a prefix pass over the groups' shared pages (each
 // group's members' query rows as one virtual sequence whose keys end at the
 // prefix) into a normalised fp32 state, then a suffix pass per sequence from
@@ -396,6 +429,9 @@ struct CascadePlan {
 int check_cascade(const mvr_paged_attention_args* a, const mvr_cascade_groups* g) {
   int rc = check_scalars(a);
   if (rc != MVR_OK) return rc;
+  if (a->page_size % mvr::kChunkTokens != 0)
+    return fail(MVR_E_UNSUPPORTED, "cascade attention needs a page_size that is a multiple of %d, not %d",
+                mvr::kChunkTokens, a->page_size);
   if (!g) return fail(MVR_E_INVALID_ARGUMENT, "groups is null");
   if (g->num_groups < 0 || g->num_groups > a->num_seqs)
     return fail(MVR_E_INVALID_ARGUMENT, "num_groups %d is outside [0, num_seqs]", g->num_groups);
@@ -596,6 +632,7 @@ int mvr_rope_append_validate(const mvr_rope_append_args* a, const int32_t* block
 
 size_t mvr_paged_attention_workspace_size(const mvr_paged_attention_args* args) {
   if (check_scalars(args) != MVR_OK) return 0;
+  if (args->page_size % mvr::kChunkTokens != 0) return make_repack_plan(args, nullptr).total;
   return make_plan(args).partial_bytes;
 }
 
@@ -604,6 +641,18 @@ int mvr_paged_attention(const mvr_paged_attention_args* a) {
   g_last_error[0] = 0;
   int rc = check_scalars(a);
   if (rc != MVR_OK) return rc;
+  if (a->page_size % mvr::kChunkTokens != 0) {
+    const RepackPlan r = make_repack_plan(a, static_cast<char*>(a->workspace));
+    rc = check_workspace(a, r.total);
+    if (rc != MVR_OK) return rc;
+    const int es = a->dtype == MVR_DTYPE_F16 ? 2 : 4;
+    hipError_t err = mvr::launch_repack_pages(
+        a->key_pool, a->value_pool, a->block_tables, a->max_pages_per_seq, a->seq_lens, a->max_seq_len, a->num_seqs,
+        a->num_kv_heads, a->page_size, a->head_dim, es, r.pages16, const_cast<void*>(r.a16.key_pool),
+        const_cast<void*>(r.a16.value_pool), const_cast<int32_t*>(r.a16.block_tables), static_cast<hipStream_t>(a->stream));
+    if (err != hipSuccess) return fail(MVR_E_HIP, "kernel launch failed: %s", hipGetErrorString(err));
+    return launch_planned(&r.a16, r.plan, static_cast<char*>(a->workspace) + r.off_part, CascadePass());
+  }
   const mvr::PagedAttentionPlan plan = make_plan(a);
   rc = check_workspace(a, plan.partial_bytes);
   if (rc != MVR_OK) return rc;

@@ -74,7 +74,7 @@ def _call(a):
     ("num_seqs", 0, M.MVR_E_INVALID_ARGUMENT, "forward requires at least one request"),
     ("num_kv_heads", 5, M.MVR_E_INVALID_ARGUMENT, "not a multiple"),
     ("head_dim", 96, M.MVR_E_UNSUPPORTED, "head_dim"),
-    ("page_size", 24, M.MVR_E_UNSUPPORTED, "page_size"),
+    ("page_size", 0, M.MVR_E_INVALID_ARGUMENT, "page_size must be positive"),
     ("max_q_len", 0, M.MVR_E_INVALID_ARGUMENT, "at least one token"),
     ("max_pages_per_seq", 60, M.MVR_E_PAGES_UNCOVERED, "leaving 64 tokens uncovered"),
     ("q", 1 + (1 << 20), M.MVR_E_INVALID_ARGUMENT, "aligned"),
@@ -95,6 +95,24 @@ def test_workspace_too_small_is_rejected():
     a.workspace_bytes = need - 1
     rc, err = _call(a)
     assert rc == M.MVR_E_WORKSPACE and "smaller than" in err
+
+
+def test_page_sizes_off_16_are_repacked_in_the_workspace():
+    # A page size that is not a multiple of 16 (the reference's own tests use 2 and 3) is accepted: the call
+    # repacks each sequence's tokens into 16-token pages in the workspace, then runs the plan of that layout.
+    a16 = _args(max_seq_len=1024)
+    p16 = M.workspace_size(a16)
+    a3 = _args(max_seq_len=1024, page_size=3, max_pages_per_seq=342)
+    need = M.workspace_size(a3)
+    pool = 2 * 64 * 8 * 16 * 128 * 2  # sequences x pages16 x kv heads x 16 tokens x head_dim x f16
+    assert need >= 2 * pool + 2 * 64 * 4 + p16
+    a3.workspace = 1 << 20
+    a3.workspace_bytes = need - 1
+    rc, err = _call(a3)
+    assert rc == M.MVR_E_WORKSPACE and "smaller than" in err
+    # A page size that does not cover max_seq_len is still the reference's error.
+    rc, err = _call(_args(max_seq_len=1024, page_size=3, max_pages_per_seq=300))
+    assert rc == M.MVR_E_PAGES_UNCOVERED and "leaving 124 tokens uncovered" in err
 
 
 def test_block_merge_plan_needs_no_workspace():

@@ -105,20 +105,28 @@ def test_reference_unit_tests_on_gpu():
         assert out.dtype == dt  # common.rs:1095-1123: dtype preserved
 
 
+@pytest.mark.parametrize("page_size", [3, 16])
 @pytest.mark.parametrize("dtype", ["f32", "f16"])
-def test_reference_paged_fixture_semantics_on_gpu(dtype):
-    """common.rs:1143-1203 at page size 16: the 5 fixture tokens sit in physical page 2 (block table [2, 0]), the
-    slots past them hold poison 99 and the pages off the table hold 88; GQA 2:1, cached_kv_len 3, q_len 2.
+def test_reference_paged_fixture_semantics_on_gpu(dtype, page_size):
+    """common.rs:1143-1203: block table [2, 0], GQA 2:1, cached_kv_len 3, q_len 2.  At the fixture's own page
+    size 3 (common.rs:1176), tokens 0-2 fill physical page 2 and tokens 3-4 the first slots of page 0, whose last
+    slot holds poison 99; at page size 16 all five sit in page 2 with 99 past them.  Pages off the table hold 88.
     F32 must reproduce the fixture's expected output; F16 (inputs rounded to f16) the oracle's."""
     case = [c for c in json.load(open(GOLDEN))["cases"] if "paged" in c][0]
     dt = torch.float16 if dtype == "f16" else torch.float32
-    D, P = 64, 16
+    D, P = 64, page_size
     kp = np.full((3, 1, 1, P, D), 88.0, np.float32)
     vp = np.full((3, 1, 1, P, D), 88.0, np.float32)
-    kp[2], vp[2] = 0.0, 0.0
-    kp[2, 0, 0, 5:], vp[2, 0, 0, 5:] = 99.0, 99.0
-    kp[2, 0, 0, :5, :2] = np.array(case["k"], np.float32).reshape(5, 2)
-    vp[2, 0, 0, :5, :2] = np.array(case["v"], np.float32).reshape(5, 2)
+    k5 = np.array(case["k"], np.float32).reshape(5, 2)
+    v5 = np.array(case["v"], np.float32).reshape(5, 2)
+    for pool, vals in ((kp, k5), (vp, v5)):
+        for page in (2, 0):
+            pool[page] = 0.0
+        for t in range(5):
+            page, slot = (2, 0)[t // P], t % P
+            pool[page, 0, 0, slot, :2] = vals[t]
+        for t in range(5, 2 * P):
+            pool[(2, 0)[t // P], 0, 0, t % P] = 99.0  # unused slots of the table's pages
     q = np.zeros((2, 2, D), np.float32)
     q[:, :, :2] = np.array(case["q"], np.float32).reshape(2, 2, 2)
     bt = np.array([[2, 0]], np.int32)
@@ -133,7 +141,7 @@ def test_reference_paged_fixture_semantics_on_gpu(dtype):
         np.testing.assert_allclose(got[:, :, :2].reshape(-1), case["expected"], atol=1e-5, rtol=0)
     else:
         args = (q[None, :, :, :2].astype(np.float16), kp[..., :2].astype(np.float16), vp[..., :2].astype(np.float16),
-                [2], P, 5, 2, 1, 2, 3, 2)
+                [2, 0][:math.ceil(5 / P)], P, 5, 2, 1, 2, 3, 2)
         ref = O.forward_paged_attention(*args, dtype=O.F16)
         exact = O.forward_paged_attention(*args, dtype=O.F16, mode=O.EXACT_F64)
         # Outputs here are 4..6, where one f16 ulp is 3.9e-3: the 2e-3 bar scales with |output| above 1.
@@ -378,3 +386,57 @@ def test_poisoned_tail_slots_and_foreign_pages_are_ignored():
 
 if __name__ == "__main__" and len(sys.argv) > 1 and sys.argv[1] == "many-partitions-child":
     _many_partitions_child()
+
+
+def _same_tokens_two_page_sizes(seed, dtype, hq, hkv, d, seq_lens, q_lens, page_size):
+    """The same logical keys and values stored once in page_size-token pages and once in 16-token pages (each with
+    its own random page order), with the queries and the two block tables."""
+    rng = np.random.default_rng(seed)
+    npd = np.float16 if dtype == "f16" else np.float32
+    seq_lens = np.asarray(seq_lens, np.int32)
+    q = (rng.standard_normal((hq, int(np.sum(q_lens)), d)) * 0.3).astype(npd)
+    toks = [(rng.standard_normal((2, int(L), hkv, d)) * 0.3).astype(npd) for L in seq_lens]
+    layouts = []
+    for P in (page_size, 16):
+        need = [math.ceil(int(L) / P) for L in seq_lens]
+        n_pages = sum(need) + 3
+        perm = rng.permutation(n_pages).astype(np.int32)
+        kp = np.full((n_pages, 1, hkv, P, d), 77.0, npd)  # slots past a sequence hold junk
+        vp = np.full((n_pages, 1, hkv, P, d), 77.0, npd)
+        bt = np.zeros((len(seq_lens), max(need)), np.int32)
+        used = 0
+        for s, L in enumerate(seq_lens.tolist()):
+            bt[s, :need[s]] = perm[used:used + need[s]]
+            used += need[s]
+            for t in range(L):
+                kp[bt[s, t // P], 0, :, t % P] = toks[s][0, t]
+                vp[bt[s, t // P], 0, :, t % P] = toks[s][1, t]
+        layouts.append((P, kp, vp, bt))
+    return q, layouts
+
+
+@pytest.mark.parametrize("page_size", [2, 3, 5, 24, 40])
+@pytest.mark.parametrize("dtype,hq,hkv,d", [("f16", 32, 8, 128), ("f32", 14, 2, 64)])
+def test_page_sizes_off_16_match_oracle_and_16_token_pages(page_size, dtype, hq, hkv, d):
+    # Decode and verify rows in one ragged batch; page sizes that are not a multiple of 16 are repacked into
+    # 16-token pages in the workspace, so the result equals the same tokens stored in 16-token pages bit for bit.
+    q_lens = [1, 5, 1, 3]
+    seq_lens = [37 + page_size, 700, 1 + 2 * page_size, 333]
+    q, layouts = _same_tokens_two_page_sizes(900 + page_size, dtype, hq, hkv, d, seq_lens, q_lens, page_size)
+    outs = []
+    for P, kp, vp, bt in layouts:
+        out = M.paged_attention(torch.from_numpy(q).cuda(), torch.from_numpy(kp).cuda(), torch.from_numpy(vp).cuda(),
+                                torch.from_numpy(bt).cuda(), torch.tensor(seq_lens, dtype=torch.int32).cuda(),
+                                torch.tensor(np.concatenate([[0], np.cumsum(q_lens)]), dtype=torch.int32).cuda(),
+                                max_q_len=max(q_lens), max_seq_len=max(seq_lens), sum_seq_lens=int(sum(seq_lens)))
+        torch.cuda.synchronize()
+        outs.append(out.cpu().numpy())
+    P, kp, vp, bt = layouts[0]
+    ref = O.paged_attention(q, kp, vp, bt, np.asarray(seq_lens, np.int32),
+                            np.concatenate([[0], np.cumsum(q_lens)]).astype(np.int32), hq, hkv, d, P,
+                            dtype=O.F16 if dtype == "f16" else O.F32, num_threads=16)
+    err = float(np.abs(outs[0].astype(np.float64) - ref).max())
+    view = np.uint16 if dtype == "f16" else np.uint32
+    diff = int(np.count_nonzero(outs[0].view(view) != outs[1].view(view)))
+    say(f"[page size {page_size}] {dtype} D={d}: max-abs vs oracle {err:.3e}; {diff} outputs differ from 16-token pages")
+    assert err <= (2e-3 if dtype == "f16" else 1e-5) and diff == 0
