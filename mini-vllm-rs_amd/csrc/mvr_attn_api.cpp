@@ -235,26 +235,14 @@ mvr::PagedAttentionPlan make_plan(const mvr_paged_attention_args* a, bool allow_
     dense = est_live * 10 < (int64_t)a->num_seqs * plan.max_parts * 7; // live fraction < 0.7
   }
   plan.dense_parts = dense;
-  if (plan.max_parts > 1 && !plan.block_merge && !plan.dense_parts) {
-    // Pad so that one sequence's units fill a multiple of 8 blocks of 4
-    // wavefronts: then (row tile, partition, KV head) maps to the same XCD
-    // for every sequence (the padding units exit at once).
-    const int per_part = plan.row_tiles * a->num_kv_heads;
-    int g = 32, x = per_part % 32;
-    while (x) { const int t = g % x; g = x; x = t; } // g = gcd(per_part, 32)
-    const int step = 32 / g;
-    int64_t mult = (plan.max_parts + step - 1) / step;
-    // Each XCD then takes mult * step * per_part / 32 blocks per sequence.
-    // When the launch gives an XCD more blocks than it has CUs, make that
-    // count odd: with an even count (8 per sequence on 16 sequences of
-    // 1K..16K tokens, whose late partitions are mostly empty) the live
-    // blocks piled onto part of the XCD's CUs, 118 us against 95 us at 7 or
-    // 9.  Below that, padding only adds blocks: 8 sequences at 4 blocks per
-    // XCD ran 14.4 us, at 5 15.3 us.
-    const int64_t xcd_blocks = mult * step * per_part / 32;
-    if (xcd_blocks % 2 == 0 && (int64_t)a->num_seqs * xcd_blocks > device_cus() / 8) mult++;
-    plan.max_parts = (int)(mult * step);
-  }
+  // No padding of max_parts.  Padding it to a multiple of 32 / gcd(Hkv * row
+  // tiles, 32) made partition p of every sequence run on the same XCD (so
+  // that pages shared by several sequences would meet in one L2), but the
+  // padded partitions are empty and always land on the same XCDs: 128
+  // sequences x 8K tokens (2 partitions padded to 4) left four XCDs idle,
+  // 3,925 GB/s against 5,683 unpadded, and 48, 96 and 128 sequences gained
+  // 34-52% at 512..8K tokens.  Unpadded was equal or better on every other
+  // workload measured, the verify workload with its shared prefixes included.
   plan.num_units = base_units * plan.max_parts;
   plan.partial_bytes = 0;
   if (plan.max_parts > 1 && !plan.block_merge) {

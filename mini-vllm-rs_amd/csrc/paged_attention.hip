@@ -377,11 +377,8 @@ __global__ __launch_bounds__(kWaveSize* kWavesPerBlock, Tr::template min_blocks<
   T* lds = lds_all[wave];
 
   // KV head fastest: the wavefronts of one (sequence, partition) read the
-  // adjacent per-head slabs of the same pages at about the same time.  The
-  // planner pads max_parts so that a sequence spans a multiple of 8 blocks:
-  // the dispatcher deals blocks to the 8 XCDs round-robin, so partition
-  // `part` of KV head h runs on the same XCD for every sequence, and pages
-  // shared by several sequences (a common prefix) hit in that XCD's L2.
+  // adjacent per-head slabs of the same pages at about the same time, and
+  // the dispatcher deals consecutive blocks to the 8 XCDs round-robin.
   // (Dealing each XCD's blocks partition-major across sequences instead
   // measured slower: 142 vs 110 us on 16 sequences of 1K..16K tokens.)
   // BM: block = (sequence, row tile, KV head) with the KV head fastest, so
