@@ -247,8 +247,9 @@ def main():
                     help="time only this one of the other workloads and print its result (for profiling one kernel)")
     a = ap.parse_args()
     if a.gpus != 1:
-        print(f"bench.py measures one GPU only; --gpus {a.gpus} is not supported (this path is single-GPU; "
-              "see the sharding notes in DESIGN.md)", file=sys.stderr)
+        print(f"bench.py measures one GPU only; --gpus {a.gpus} is not supported: the attention path runs on one "
+              "GPU per call (a multi-GPU deployment shards sequences or KV heads across GPUs, each GPU running "
+              "its own share)", file=sys.stderr)
         sys.exit(2)
 
     import torch
