@@ -440,3 +440,49 @@ def test_page_sizes_off_16_match_oracle_and_16_token_pages(page_size, dtype, hq,
     diff = int(np.count_nonzero(outs[0].view(view) != outs[1].view(view)))
     say(f"[page size {page_size}] {dtype} D={d}: max-abs vs oracle {err:.3e}; {diff} outputs differ from 16-token pages")
     assert err <= (2e-3 if dtype == "f16" else 1e-5) and diff == 0
+
+
+@pytest.mark.parametrize("page_size,seq_len,q_len", [(16, 8192, 1), (16, 1000, 1), (5, 700, 1), (16, 1000, 200)])
+def test_pages_past_2_pow_31_elements(page_size, seq_len, q_len):
+    # Page ids above 2^31 / (Hkv * page_size * D) put their elements past 2^31 in the pool, so every offset must
+    # be 64-bit: the split-context kernel (1000 tokens, ragged pair), the block-merge launch (two uniform 8K
+    # sequences: 4 partitions), the repack of odd page sizes and the prefill kernel (200-token chunks).  The
+    # pools are ~4 GiB each on the device, with only the used pages written; the oracle sees a compact host copy
+    # of those pages.
+    hq, hkv, d, n = 32, 8, 128, 2
+    stride = hkv * page_size * d
+    first = (1 << 31) // stride + 7
+    lens = [seq_len, seq_len if seq_len == 8192 else seq_len // 2 + 3]
+    need = [math.ceil(L / page_size) for L in lens]
+    rng = np.random.default_rng(17 + page_size + q_len)
+    ids = first + rng.permutation(sum(need) + 3)[:sum(need)].astype(np.int64)
+    num_pages = int(ids.max()) + 1
+    assert int(ids.min()) * stride > (1 << 31)
+    bt = np.zeros((n, max(need)), np.int32)
+    bt[0, :need[0]] = ids[:need[0]]
+    bt[1, :need[1]] = ids[need[0]:]
+    kp = torch.empty((num_pages, 1, hkv, page_size, d), dtype=torch.float16, device="cuda")
+    vp = torch.empty_like(kp)
+    used = torch.from_numpy(ids).cuda()
+    g = torch.Generator(device="cuda").manual_seed(5)
+    kvals = (torch.randn((len(ids), 1, hkv, page_size, d), generator=g, device="cuda") * 0.3).half()
+    vvals = (torch.randn((len(ids), 1, hkv, page_size, d), generator=g, device="cuda") * 0.3).half()
+    kp[used] = kvals
+    vp[used] = vvals
+    cu = np.array([0, q_len, 2 * q_len], np.int32)
+    q = (torch.randn((hq, n * q_len, d), generator=g, device="cuda") * 0.3).half()
+    out = M.paged_attention(q, kp, vp, torch.from_numpy(bt).cuda(), torch.tensor(lens, dtype=torch.int32).cuda(),
+                            torch.from_numpy(cu).cuda(), max_q_len=q_len, max_seq_len=max(lens),
+                            sum_seq_lens=int(sum(lens)))
+    torch.cuda.synchronize()
+    # Oracle on a compact pool: page ids[i] -> i.
+    remap = {int(v): i for i, v in enumerate(ids)}
+    bt_c = np.vectorize(lambda x: remap.get(int(x), 0))(bt).astype(np.int32)
+    ref = O.paged_attention(q.cpu().numpy(), kvals.cpu().numpy(), vvals.cpu().numpy(), bt_c,
+                            np.asarray(lens, np.int32), cu, hq, hkv, d, page_size, dtype=O.F16, num_threads=16)
+    err = float(np.abs(out.float().cpu().numpy() - ref).max())
+    say(f"[2^31] page size {page_size}, lengths {lens}, q_len {q_len}: pool {num_pages} pages, "
+        f"max-abs vs oracle {err:.3e}")
+    del kp, vp
+    torch.cuda.empty_cache()
+    assert err <= 2e-3
