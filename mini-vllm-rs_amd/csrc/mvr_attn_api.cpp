@@ -235,6 +235,18 @@ mvr::PagedAttentionPlan make_plan(const mvr_paged_attention_args* a, bool allow_
     dense = est_live * 10 < (int64_t)a->num_seqs * plan.max_parts * 7; // live fraction < 0.7
   }
   plan.dense_parts = dense;
+  // Deep pipeline (three chunks in flight per wavefront) for the ragged plans
+  // that keep slot == partition: their live wavefronts (planned at 80% of the
+  // resident slots) do not fill the device and wait on load latency.  Measured
+  // on F16 D=128 decode: ragged 8..16 sequences of up to 8K..32K tokens 14-19%
+  // faster, 32 x 4K 5%, 24 x 12K and 16 x 32K unchanged; uniform batches gain
+  // nothing, and short partitions (< 8 chunks: a 512-token F32 sequence, 8
+  // Qwen2-0.5B sequences) lose 1-5% to the extra tail loads, so neither takes it.
+  // MVR_ATTN_DEEP_PIPELINE=false turns it off.
+  static const bool deep_enabled = env_bool("MVR_ATTN_DEEP_PIPELINE", true);
+  const int elem_bytes = a->dtype == MVR_DTYPE_F16 ? 2 : 4;
+  plan.deep_pipeline = deep_enabled && ragged && !dense && !plan.block_merge && plan.row_blocks == 1 &&
+                       a->head_dim * elem_bytes <= 256 && plan.chunks_per_part >= 8;
   // No padding of max_parts.  Padding it to a multiple of 32 / gcd(Hkv * row
   // tiles, 32) made partition p of every sequence run on the same XCD (so
   // that pages shared by several sequences would meet in one L2), but the

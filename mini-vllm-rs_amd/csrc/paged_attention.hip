@@ -19,7 +19,7 @@
 //     returns V^T in the A-operand layout, O^T += V^T P^T with
 //     v_mfma_f32_16x16x16_f16 (f32: ds_read_b32 + v_mfma_f32_16x16x4_f32).
 // Loads for chunk k+2 are issued before chunk k is consumed (two chunks in
-// flight per wavefront).  Partitions of one (b, h, rt) are merged by
+// flight per wavefront; three for the plans that ask for a deep pipeline).  Partitions of one (b, h, rt) are merged by
 // merge_partitions_kernel with the usual max / sum-of-exponentials rescale.
 #include "paged_attention_kernels.hpp"
 
@@ -358,11 +358,18 @@ struct F32Traits {
 // the block's barrier.
 // DENSE: the dense layout of a ragged batch (dense_unit); a separate instantiation,
 // so that the slot == partition kernels compile exactly as without it.
-template <typename Tr, int D, int NB, bool BM = false, bool DENSE = false>
-__global__ __launch_bounds__(kWaveSize* kWavesPerBlock, Tr::template min_blocks<NB>()) void paged_attention_kernel(
-    PagedAttentionParams p) {
+// DEPTH: chunks in flight per wavefront.  3 (deep_pipeline plans: 16-row
+// tiles whose K and V chunk take 32 VGPRs per lane) costs 192-208 VGPRs, so two
+// wavefronts per SIMD instead of three; that pays on ragged batches of few
+// sequences, whose live wavefronts do not fill the device and wait on
+// latency (16 sequences of 1.9K..14.8K tokens: 120 -> 106 us), and loses
+// where a third wavefront per SIMD had work (128 ragged sequences).
+template <typename Tr, int D, int NB, bool BM = false, bool DENSE = false, int DEPTH = 2>
+__global__ __launch_bounds__(kWaveSize* kWavesPerBlock, DEPTH == 3 ? 2 : Tr::template min_blocks<NB>()) void
+    paged_attention_kernel(PagedAttentionParams p) {
   typedef typename Tr::elem T;
   constexpr int kTileRows = 16 * NB;
+  static_assert(DEPTH == 2 || (DEPTH == 3 && NB == 1 && D * sizeof(T) <= 256 && !BM), "unsupported pipeline depth");
   __shared__ __attribute__((aligned(16))) T lds_all[kWavesPerBlock][kChunkTokens * D];
   // BM: each wavefront's rows (O, m, l); rows padded by 4 floats so that the
   // 16 rows of a float4 store fall in distinct banks.
@@ -514,18 +521,21 @@ __global__ __launch_bounds__(kWaveSize* kWavesPerBlock, Tr::template min_blocks<
     Tr::load_v(vpool + off, l, vr);
   };
 
-  typename Tr::kreg_t ka[Tr::kLoads], kb[Tr::kLoads];
-  typename Tr::vreg_t va[Tr::kLoads], vb[Tr::kLoads];
+  // DEPTH chunks in flight; a tail past k1 reloads chunk k1 - 1 (an L2 hit)
+  // rather than branching.
+  typename Tr::kreg_t kbuf[DEPTH][Tr::kLoads];
+  typename Tr::vreg_t vbuf[DEPTH][Tr::kLoads];
   if (k0 < k1) { // always, except a BM partition without keys (its chunks lie past the table)
-    load_chunk(k0, ka, va);
-    load_chunk(min(k0 + 1, k1 - 1), kb, vb);
+#pragma unroll
+    for (int i = 0; i < DEPTH; i++) load_chunk(min(k0 + i, k1 - 1), kbuf[i], vbuf[i]);
   }
-  for (int k = k0; k < k1; k += 2) {
-    process(k, ka, va);
-    load_chunk(min(k + 2, k1 - 1), ka, va);
-    if (k + 1 < k1) {
-      process(k + 1, kb, vb);
-      load_chunk(min(k + 3, k1 - 1), kb, vb);
+  for (int k = k0; k < k1; k += DEPTH) {
+#pragma unroll
+    for (int i = 0; i < DEPTH; i++) {
+      if (i == 0 || k + i < k1) {
+        process(k + i, kbuf[i], vbuf[i]);
+        load_chunk(min(k + i + DEPTH, k1 - 1), kbuf[i], vbuf[i]);
+      }
     }
   }
 
@@ -761,6 +771,13 @@ hipError_t launch_typed(const PagedAttentionPlan& plan, const PagedAttentionPara
     if (params.row_tiles != 1) return hipErrorInvalidValue; // dense_unit walks row tile 0 only
     hipLaunchKernelGGL((paged_attention_kernel<Tr, D, NB, false, true>), dim3((unsigned)blocks),
                        dim3(kWaveSize * kWavesPerBlock), 0, stream, params);
+  } else if (plan.deep_pipeline) {
+    if constexpr (NB == 1 && D * sizeof(typename Tr::elem) <= 256) {
+      hipLaunchKernelGGL((paged_attention_kernel<Tr, D, NB, false, false, 3>), dim3((unsigned)blocks),
+                         dim3(kWaveSize * kWavesPerBlock), 0, stream, params);
+    } else {
+      return hipErrorInvalidValue; // planned only where the registers allow three chunks in flight
+    }
   } else {
     hipLaunchKernelGGL((paged_attention_kernel<Tr, D, NB>), dim3((unsigned)blocks), dim3(kWaveSize * kWavesPerBlock),
                        0, stream, params);

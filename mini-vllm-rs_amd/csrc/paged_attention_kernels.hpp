@@ -65,6 +65,7 @@ struct PagedAttentionPlan {
   int kv_splits;        // prefill: key-range splits per 128-row tile
   bool block_merge;     // max_parts == kWavesPerBlock: one block per tile, partitions merged in LDS
   bool dense_parts;     // ragged split plan: live units first, in a dense order (see dense_unit)
+  bool deep_pipeline;   // three chunks in flight per wavefront instead of two (16-row tiles only)
 };
 
 hipError_t launch_paged_attention(const PagedAttentionPlan& plan, PagedAttentionParams params, hipStream_t stream);
