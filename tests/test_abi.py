@@ -87,6 +87,39 @@ def test_scalar_checks_reject_before_launch(field, value, code, msg):
     assert msg in err
 
 
+def test_errors_are_per_thread_under_concurrent_calls():
+    # Several backends (one OS thread each, server/mod.rs:380-391) may call the library at once; each
+    # thread must read back its own error.  ctypes drops the GIL around foreign calls, so the
+    # threads' checks and error writes overlap in the library.
+    import threading
+    cases = [("dtype", 7, M.MVR_E_UNSUPPORTED, "dtype"),
+             ("num_kv_heads", 5, M.MVR_E_INVALID_ARGUMENT, "not a multiple"),
+             ("head_dim", 96, M.MVR_E_UNSUPPORTED, "head_dim"),
+             ("max_pages_per_seq", 60, M.MVR_E_PAGES_UNCOVERED, "leaving 64 tokens uncovered"),
+             ("q_stride_token", 100, M.MVR_E_INVALID_ARGUMENT, "aligned"),
+             ("seq_lens", None, M.MVR_E_INVALID_ARGUMENT, "required"),
+             ("max_q_len", 0, M.MVR_E_INVALID_ARGUMENT, "at least one token"),
+             ("page_size", 0, M.MVR_E_INVALID_ARGUMENT, "page_size must be positive")]
+    start = threading.Barrier(len(cases))
+    failures = []
+
+    def worker(field, value, code, msg):
+        a = _args(**{field: value})
+        start.wait()
+        for _ in range(300):
+            rc, err = _call(a)
+            if rc != code or msg not in err:
+                failures.append((field, rc, err))
+                return
+
+    threads = [threading.Thread(target=worker, args=c) for c in cases]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join()
+    assert not failures, failures[:3]
+
+
 def test_workspace_too_small_is_rejected():
     a = _args(max_seq_len=1024)
     need = M.workspace_size(a)
