@@ -165,6 +165,8 @@ mvr::PagedAttentionPlan make_plan(const mvr_paged_attention_args* a, bool allow_
   const int64_t base_units = (int64_t)a->num_seqs * a->num_kv_heads * plan.row_tiles;
   const bool ragged = a->sum_seq_lens > 0 && a->sum_seq_lens < (int64_t)a->max_seq_len * a->num_seqs;
   int cpp = chunks_per_partition_override();
+  // Kept for a dense ragged plan, which re-splits at a higher fill below.
+  int64_t ragged_units_per_group = 0, ragged_total_chunks = 0, ragged_floor = 0;
   if (cpp <= 0) {
     // Split contexts so that the units fill the resident wavefront slots of
     // the device once: more partitions add merge traffic and a tail round,
@@ -198,6 +200,11 @@ mvr::PagedAttentionPlan make_plan(const mvr_paged_attention_args* a, bool allow_
     // F32 sequence and 24 -> 14 us on 8 sequences of 128..4096 tokens.
     const int64_t floor_cpp = max_chunks <= 64 ? 2 : 4;
     cpp = (int)(c < floor_cpp ? floor_cpp : (c > max_chunks ? max_chunks : c));
+    if (ragged) {
+      ragged_units_per_group = units_per_group;
+      ragged_total_chunks = (a->sum_seq_lens + mvr::kChunkTokens - 1) / mvr::kChunkTokens + a->num_seqs / 2;
+      ragged_floor = floor_cpp;
+    }
   }
   if (cpp > max_chunks) cpp = max_chunks;
   plan.chunks_per_part = cpp;
@@ -235,6 +242,22 @@ mvr::PagedAttentionPlan make_plan(const mvr_paged_attention_args* a, bool allow_
     dense = est_live * 10 < (int64_t)a->num_seqs * plan.max_parts * 7; // live fraction < 0.7
   }
   plan.dense_parts = dense;
+  if (dense && ragged_units_per_group > 0 && max_chunks > 64) {
+    // Dense plans split for 120% of the resident slots instead of 80%:
+    // in-order dispatch hands the extra units to whichever CU frees first,
+    // and the layout has already given up the cross-sequence partition
+    // alignment that more, shorter units would break.  Measured (F16 D=128
+    // decode, U[L/8, L]): 128 x 8K 494 -> 440 us, 128 x 16K 1001 -> 901,
+    // 32 x 4K 69 -> 65, 64 x 2K 73 -> 70; contexts up to 1K tokens (their
+    // 2-chunk floor) lost 5% (256 x 512), so they keep 80%.
+    int64_t u = ragged_units_per_group * 6 / 5;
+    if (u < 1) u = 1;
+    int64_t c = (ragged_total_chunks + u - 1) / u;
+    if (c < ragged_floor) c = ragged_floor;
+    if (c > max_chunks) c = max_chunks;
+    plan.chunks_per_part = (int)c;
+    plan.max_parts = (max_chunks + plan.chunks_per_part - 1) / plan.chunks_per_part;
+  }
   // Deep pipeline (three chunks in flight per wavefront) for the ragged plans
   // that keep slot == partition: their live wavefronts (planned at 80% of the
   // resident slots) do not fill the device and wait on load latency.  Measured

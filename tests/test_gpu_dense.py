@@ -6,12 +6,17 @@ lets each wavefront find its unit with a wave-wide scan of the sequence
 lengths (dense_unit).  Same bar as every call: 2e-3 (F16) / 1e-5 (F32)
 against the oracle.  Covers 64 sequences of 257..2049 tokens (F16, D=128), 150
 sequences of 17..1024 tokens (more than one 64-sequence block of the scan, the
-F16 D=64 kernel) and 40 F32 sequences.  The dense layout only changes which
-wavefront computes which partition, so the result is also compared bit for bit
-with the slot == partition layout of the same batch, computed in a child
-process with MVR_ATTN_DENSE_RAGGED=false (the flag is read once per process;
-these batches take the dense layout by the planner's rule: at least 32
-sequences, estimated live fraction of the slot grid below 0.7).
+F16 D=64 kernel) and 40 F32 sequences.  By default a dense plan also splits
+contexts into more partitions than the slot == partition plan of the same
+batch (a higher fill target), which changes the rounding.  With the same
+partitions the dense layout only changes which wavefront computes which
+partition, so two child processes run the batch at a fixed number of chunks
+per partition (MVR_ATTN_CHUNKS_PER_PARTITION, which also skips the re-split),
+one with the dense layout and one with MVR_ATTN_DENSE_RAGGED=false, and the
+results are compared bit for bit.  (The flags are read once per process; at
+8 and 4 chunks per partition these batches take the dense layout by the
+planner's rule: at least 32 sequences, estimated live fraction of the slot
+grid below 0.7.)
 """
 import os
 import subprocess
@@ -87,8 +92,8 @@ def test_dense_matches_oracle(name):
     assert np.isfinite(got).all() and err <= TOL[w.dtype], err
 
 
-def _slot_layout_child(name, path):
-    """Child-process side: the same batch with the dense layout switched off."""
+def _layout_child(name, path):
+    """Child-process side: the batch under the environment the parent chose."""
     M.load_library()
     out, need = _attend(_case(name))
     np.save(path, out)
@@ -99,26 +104,32 @@ _CHILD = (
     "import sys\n"
     "sys.path[:0] = sys.argv[3].split('|')\n"
     "import test_gpu_dense as T\n"
-    "T._slot_layout_child(sys.argv[1], sys.argv[2])\n"
-    "print('slot layout done', flush=True)\n"
+    "T._layout_child(sys.argv[1], sys.argv[2])\n"
+    "print('layout done', flush=True)\n"
 )
 
 
-@pytest.mark.parametrize("name", ["f16-d128-64x[257,2049]", "f16-d64-150x[17,1024]"])
-def test_dense_bit_identical_to_slot_layout(name, tmp_path):
-    got, need = _attend(_case(name))
+FIXED_CHUNKS = {"f16-d128-64x[257,2049]": "8", "f16-d64-150x[17,1024]": "4"}
+
+
+def _run_child(name, dst, **env):
     here = os.path.dirname(os.path.abspath(__file__))
     root = os.path.dirname(here)
     paths = "|".join([here, root, os.path.join(root, "oracle"), os.path.join(root, "mini-vllm-rs_amd")])
-    dst = str(tmp_path / "slot_layout.npy")
-    say(f"[dense] {name}: slot == partition layout in a child process (MVR_ATTN_DENSE_RAGGED=false)")
-    child = subprocess.run([sys.executable, "-c", _CHILD, name, dst, paths],
-                           env=dict(os.environ, MVR_ATTN_DENSE_RAGGED="false"), capture_output=True, text=True,
-                           timeout=180)
+    child = subprocess.run([sys.executable, "-c", _CHILD, name, dst, paths], env=dict(os.environ, **env),
+                           capture_output=True, text=True, timeout=180)
     assert child.returncode == 0, child.stdout[-2000:] + child.stderr[-2000:]
-    ref = np.load(dst)
-    ref_ws = int(np.load(dst + ".ws.npy")[0])
-    # Both layouts hold the same partitions (the same chunks per partition), so the same workspace.
+    return np.load(dst), int(np.load(dst + ".ws.npy")[0])
+
+
+@pytest.mark.parametrize("name", list(FIXED_CHUNKS))
+def test_dense_bit_identical_to_slot_layout(name, tmp_path):
+    cpp = FIXED_CHUNKS[name]
+    say(f"[dense] {name}: dense and slot == partition layouts at {cpp} chunks per partition (child processes)")
+    got, need = _run_child(name, str(tmp_path / "dense.npy"), MVR_ATTN_CHUNKS_PER_PARTITION=cpp)
+    ref, ref_ws = _run_child(name, str(tmp_path / "slot.npy"), MVR_ATTN_CHUNKS_PER_PARTITION=cpp,
+                             MVR_ATTN_DENSE_RAGGED="false")
+    # Both layouts hold the same partitions, so the same workspace.
     assert need == ref_ws, (need, ref_ws)
     view = np.uint16 if got.dtype == np.float16 else np.uint32
     diff = int(np.count_nonzero(got.view(view) != ref.view(view)))
