@@ -20,6 +20,7 @@ sys.path.insert(0, os.path.join(ROOT, "mini-vllm-rs_amd"))
 
 HBM_PEAK_GBS = 8000.0      # MI355X HBM3E, 8 TB/s
 MFMA_F16_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 MFMA
+MFMA_F32_PEAK_TFLOPS = 157.3   # MI355X dense fp32 MFMA
 # HBM bytes per launch of the split-context kernel, from the FETCH_SIZE / WRITE_SIZE counter runs
 # summarised in this file (line "bytes_per_launch: N").
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "paged_attention_decode_b64_ctx8192_f16_hbm_traffic.md")
@@ -30,15 +31,17 @@ def log(msg):
 
 
 class Runner:
-    """Prebuilt C argument block for repeated calls (no per-call Python work beyond one ctypes call)."""
+    """Prebuilt C argument block for repeated calls (no per-call Python work beyond one ctypes call).
+    host_hints: also pass host copies of seq_lens / cu_q_lens (the planner's optional hints)."""
 
-    def __init__(self, w, tensors, torch, M):
+    def __init__(self, w, tensors, torch, M, host_hints=False):
         self.w = w
         self.t = tensors
         self.out = torch.empty_like(tensors["q"])
+        hints = dict(seq_lens_host=w.seq_lens, cu_q_lens_host=w.cu_q_lens) if host_hints else {}
         self.args = M.make_args(tensors["q"], tensors["key_pool"], tensors["value_pool"], tensors["block_tables"],
                                 tensors["seq_lens"], tensors["cu_q_lens"], self.out, max_q_len=w.max_q_len,
-                                max_seq_len=w.max_seq_len, sum_seq_lens=int(w.seq_lens.sum()))
+                                max_seq_len=w.max_seq_len, sum_seq_lens=int(w.seq_lens.sum()), **hints)
         need = M.workspace_size(self.args)
         self.ws = M.new_workspace(need, "cuda")
         self.args.workspace = self.ws.data_ptr()
@@ -69,6 +72,20 @@ def time_steps(runner, torch, steps, warmup):
     wall = time.perf_counter() - t0
     per = sorted(s.elapsed_time(e) * 1e3 for s, e in zip(starts, ends))  # microseconds, kernel-side
     return wall, per
+
+
+def cpu_model():
+    """The host CPU's model name (first "model name" line of /proc/cpuinfo) and its logical CPU count."""
+    name = platform.processor() or platform.machine()
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    name = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return dict(model=name, logical_cpus=os.cpu_count(), usable_cpus=len(os.sched_getaffinity(0)))
 
 
 def cpu_baseline(W):
@@ -118,11 +135,12 @@ def cpu_baseline(W):
                 single_thread=dict(value=round(one.algorithmic_bytes() / per_call1 / 1e9, 3), unit="GB/s", cores=1,
                                    sample=f"1 of {full.num_seqs} sequences x 8 kv heads x 8192 tokens, {reps1} calls, "
                                           f"{per_call1 * 1e3:.1f} ms/call"),
-                host=platform.processor() or platform.machine())
+                host=cpu_model())
 
 
 def measure(W, M, torch, cfg, steps, warmup):
-    w = W.CONFIGS[cfg]()
+    """cfg: a key of W.CONFIGS or a workload builder."""
+    w = W.CONFIGS[cfg]() if isinstance(cfg, int) else cfg()
     t = W.device_tensors(w, None)
     r = Runner(w, t, torch, M)
     wall, per = time_steps(r, torch, steps, warmup)
@@ -137,9 +155,11 @@ def measure(W, M, torch, cfg, steps, warmup):
         res["hbm_frac"] = round(res["unique_gbs"] / HBM_PEAK_GBS, 4)
     else:
         res["hbm_frac"] = round(res["eff_gbs"] / HBM_PEAK_GBS, 4)
-    if cfg == 4:
+    if w.total_q > w.num_seqs * 16:  # prefill-sized: MFMA-bound
+        peak = MFMA_F16_PEAK_TFLOPS if w.dtype == "f16" else MFMA_F32_PEAK_TFLOPS
         res["tflops"] = round(w.flops() / (med * 1e-6) / 1e12, 2)
-        res["mfma_frac"] = round(res["tflops"] / MFMA_F16_PEAK_TFLOPS, 4)
+        res["mfma_frac"] = round(res["tflops"] / peak, 4)
+        res["mfma_peak_tflops"] = peak
     del t, r
     torch.cuda.empty_cache()
     return res
@@ -220,6 +240,45 @@ def measure_cascade(W, M, torch, cfg, steps, warmup, with_plain=False):
     return res
 
 
+class SliceRunner(Runner):
+    """The call over sequences [lo, hi) of a workload alone, on the same device tensors (q / out rows of those
+    sequences; block-table rows; lengths; cu_q_lens rebased to 0)."""
+
+    def __init__(self, w, tensors, torch, M, lo, hi, W):
+        import numpy as np
+
+        cu = w.cu_q_lens
+        sub = W.Workload(f"{w.name} [{lo}:{hi}]", w.dtype, w.num_q_heads, w.num_kv_heads, w.head_dim, w.page_size,
+                         w.num_pages, w.value_scale, w.seq_lens[lo:hi].copy(), w.q_lens[lo:hi].copy(),
+                         np.ascontiguousarray(w.block_tables[lo:hi]), w.seed)
+        t = dict(tensors, q=tensors["q"][:, int(cu[lo]):int(cu[hi])],
+                 block_tables=tensors["block_tables"][lo:hi].contiguous(), seq_lens=tensors["seq_lens"][lo:hi].contiguous(),
+                 cu_q_lens=torch.from_numpy(sub.cu_q_lens).cuda())
+        super().__init__(sub, t, torch, M)
+
+
+def measure_mixed(W, M, torch, steps, warmup):
+    """One scheduler step's batch (63 decodes at 8K + a 256-token chunk on a 2K prefix, Llama-3-8B shape, F16):
+    the call planned for its longest query (no host hints), the call routed per sequence class (host copies of
+    the lengths), and its two parts timed alone on the same tensors."""
+    w = W.llama3_8b_mixed_decode_prefill_f16()
+    t = W.device_tensors(w, None)
+    n_dec = int((w.q_lens == 1).sum())
+    res = dict(workload=w.name, bytes=w.algorithmic_bytes(), flops=w.flops())
+    for key, r in (("no_hints", Runner(w, t, torch, M)), ("host_hints", Runner(w, t, torch, M, host_hints=True)),
+                   ("decodes_alone", SliceRunner(w, t, torch, M, 0, n_dec, W)),
+                   ("prefill_alone", SliceRunner(w, t, torch, M, n_dec, w.num_seqs, W))):
+        _, per = time_steps(r, torch, steps, warmup)
+        res[key + "_us"] = round(per[len(per) // 2], 2)
+        del r
+    res["sum_of_parts_us"] = round(res["decodes_alone_us"] + res["prefill_alone_us"], 2)
+    res["host_hints_gbs"] = round(w.algorithmic_bytes() / (res["host_hints_us"] * 1e-6) / 1e9, 1)
+    res["hbm_frac"] = round(res["host_hints_gbs"] / HBM_PEAK_GBS, 4)
+    del t
+    torch.cuda.empty_cache()
+    return res
+
+
 def measure_append(W, M, torch, cfg, steps, warmup):
     w = W.CONFIGS[cfg]()
     t = W.device_tensors(w, None)
@@ -245,6 +304,7 @@ def main():
                     help="also run 3 device copies of 1 GiB (a plain copy kernel of known size, for HBM counters)")
     ap.add_argument("--only-config", type=int, default=0, choices=(0, 1, 2, 4, 5),
                     help="time only this one of the other workloads and print its result (for profiling one kernel)")
+    ap.add_argument("--only-mixed", action="store_true", help="time only the mixed decode + prefill batch")
     a = ap.parse_args()
     if a.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {a.gpus} is not supported: the attention path runs on one "
@@ -261,6 +321,9 @@ def main():
         print("no GPU visible", file=sys.stderr)
         sys.exit(1)
     M.load_library()
+    if a.only_mixed:
+        print(json.dumps({"mixed": measure_mixed(W, M, torch, a.steps, a.warmup)}), flush=True)
+        return
     if a.only_config:
         log(f"[bench] config {a.only_config} only")
         res = measure(W, M, torch, a.only_config, a.steps, a.warmup)
@@ -331,6 +394,13 @@ def main():
             log(f"[bench] config {cfg}")
             per_cfg[str(cfg)] = measure(W, M, torch, cfg, max(20, a.steps // 2), a.warmup)
         result["configs"] = per_cfg
+        log("[bench] F32 (the activation dtype the reference's GPU backends force) at configs 3 and 4")
+        result["f32"] = {
+            "3": measure(W, M, torch, lambda: W.llama3_8b_decode_b64_8k_f16(64, "f32"), max(20, a.steps // 2), a.warmup),
+            "4": measure(W, M, torch, lambda: W.qwen2_7b_chunked_prefill_f16("f32"), max(20, a.steps // 2), a.warmup),
+        }
+        log("[bench] mixed decode + prefill batch")
+        result["mixed"] = measure_mixed(W, M, torch, max(20, a.steps // 2), a.warmup)
         log("[bench] config 5 through cascade attention")
         result["cascade"] = {"5": measure_cascade(W, M, torch, 5, max(20, a.steps // 2), a.warmup)}
         log("[bench] shared-prompt decode, cascade and plain")

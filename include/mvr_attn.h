@@ -27,11 +27,21 @@
  *   Query i of a request (0-based within the request) sees keys
  *     0 ..= seq_len - q_len + i (common.rs:948-965).
  *
- * Every call is stream-ordered and asynchronous, allocates nothing and keeps
- * no global mutable state besides a thread-local error string, so several
- * threads may drive several devices concurrently.  Functions return MVR_OK
- * (0) or a negative MVR_E_* code; mvr_last_error() describes the last
- * failure on the calling thread.
+ * Every call is stream-ordered and asynchronous and allocates nothing.  Its
+ * only global state is a thread-local error string, environment flags read
+ * once, and a per-device cache of the runtime's occupancy answer (atomics,
+ * each written with a value that never changes), so several threads may
+ * drive several devices concurrently.  Functions return MVR_OK (0) or a
+ * negative MVR_E_* code; mvr_last_error() describes the last failure on the
+ * calling thread.
+ *
+ * Device tables (block tables, lengths, group tables) are trusted by the
+ * launching entry points; the *_validate functions check host copies.  With
+ * MVR_ATTN_CHECKED=true in the environment (a development mode) every
+ * launching call first copies its device tables back, waits for its stream
+ * and runs those checks, returning their error instead of launching.  The
+ * kernels clamp a device seq_len above max_seq_len to max_seq_len, so such a
+ * table reads no page outside its block-table row.
  */
 #ifndef MVR_ATTN_H
 #define MVR_ATTN_H
@@ -43,7 +53,7 @@
 extern "C" {
 #endif
 
-#define MVR_ATTN_ABI_VERSION 1
+#define MVR_ATTN_ABI_VERSION 2
 
 /* ActivationDType (src/model_runner/mod.rs:331-351): F32 or F16 only. */
 typedef enum { MVR_DTYPE_F32 = 0, MVR_DTYPE_F16 = 1 } mvr_dtype;
@@ -93,6 +103,15 @@ typedef struct mvr_paged_attention_args {
   size_t workspace_bytes;
   void* stream;              /* hipStream_t; NULL = the null stream */
   int64_t sum_seq_lens;      /* optional planning hint: sum of seq_lens (0 = unknown, assume max_seq_len each) */
+  /* Optional planning hints (NULL = unknown): host copies of seq_lens [num_seqs] and cu_q_lens [num_seqs + 1]
+     holding the same values as the device tables (the caller builds them on the host before uploading; the
+     kernels read only the device tables).  With cu_q_lens_host, a batch that mixes decode-sized requests
+     (q_len * num_q_heads / num_kv_heads <= 32) with prefill-sized ones, as one scheduler step packs them
+     (scheduler.rs:258-271), runs each class as its own launch planned for it, instead of planning the whole
+     call for its longest query; seq_lens_host also sizes each class's context split exactly.  Read during
+     the call only. */
+  const int32_t* seq_lens_host;
+  const int32_t* cu_q_lens_host;
 } mvr_paged_attention_args;
 
 /* Bytes of workspace mvr_paged_attention needs for these arguments (depends

@@ -133,6 +133,10 @@ __global__ __launch_bounds__(kThreads) void rope_append_kernel(RopeAppendParams 
   }
   const int seq_len = p.seq_lens ? ((const const_i32*)p.seq_lens)[b] : p.single_seq_len;
   const int pos = seq_len - q_len + (n - q_start); // cached_kv_len + i (kv_cache/utils.rs:20-24)
+  // Positions outside [0, max_seq_len) only come from tables that break the
+  // contract (seq_len < q_len or > max_seq_len): write nothing rather than
+  // leave the block-table row, the rotary tables or the pools.
+  if (pos < 0 || pos >= p.single_seq_len) return;
   const const_i32* bt = (const const_i32*)p.block_tables + (int64_t)b * p.block_table_stride;
   const int64_t page = bt[pos / p.page_size];
   const int slot = pos % p.page_size;

@@ -11,6 +11,8 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <vector>
+
 #include "kv_append.hpp"
 #include "kv_gather.hpp"
 #include "paged_attention_kernels.hpp"
@@ -49,11 +51,39 @@ bool env_bool(const char* name, bool fallback) {
 }
 
 // roctx ranges named like the reference's tracing spans (trace.rs:64-116,
-// mirrored to NVTX by nvtx_trace.rs:14-53), on when MVR_ENABLE_ROCTX=true.
+// mirrored to NVTX by nvtx_trace.rs:14-53, whose labels are the span name
+// followed by its fields as " field=value"), on when MVR_ENABLE_ROCTX=true.
 bool roctx_enabled() {
   static const bool v = env_bool("MVR_ENABLE_ROCTX", false);
   return v;
 }
+
+// Development mode, on when MVR_ATTN_CHECKED=true: every call copies the
+// device tables it is about to trust back to the host (stream-ordered, then
+// waits for the stream) and runs the host checks of the matching *_validate
+// entry point first, so that tables breaking the contract come back as an
+// MVR_E_* error instead of wrong reads.  It synchronises the stream and
+// allocates host memory on every call: not for serving.
+bool checked_mode() {
+  static const bool v = env_bool("MVR_ATTN_CHECKED", false);
+  return v;
+}
+
+// Host copy of `count` int32 device values (none when ptr is null); false and
+// an error message if the copy fails.
+bool copy_table(const int32_t* dev, size_t count, hipStream_t stream, std::vector<int32_t>& host) {
+  host.clear();
+  if (!dev || count == 0) return true;
+  host.resize(count);
+  if (hipMemcpyAsync(host.data(), dev, count * sizeof(int32_t), hipMemcpyDeviceToHost, stream) != hipSuccess ||
+      hipStreamSynchronize(stream) != hipSuccess) {
+    (void)hipGetLastError();
+    return false;
+  }
+  return true;
+}
+
+const int32_t* ptr_or_null(const std::vector<int32_t>& v) { return v.empty() ? nullptr : v.data(); }
 
 struct TraceRange {
   bool on;
@@ -292,8 +322,10 @@ mvr::PagedAttentionPlan make_plan(const mvr_paged_attention_args* a, bool allow_
 
 namespace {
 
-// The extra inputs of one pass of cascade attention (all null / 0 for a plain call).
-struct CascadePass {
+// The extra inputs of one launch: the passes of cascade attention, and the
+// q_len class of one launch of a mixed batch (all null / 0 for a plain call).
+struct LaunchExtras {
+  int32_t class_q_min = 0, class_q_max = 0; // sequences outside [min, max] (max 0: unbounded) are skipped
   const int32_t* key_begin = nullptr; // suffix pass: first key of each sequence
   const int32_t* key_end = nullptr;   // prefix pass: keys [0, key_end) of each group
   float* state_o = nullptr;           // normalised fp32 rows instead of `out`
@@ -306,7 +338,7 @@ struct CascadePass {
 
 // Launches the planned kernel(s); workspace ws holds plan.partial_bytes.
 int launch_planned(const mvr_paged_attention_args* a, const mvr::PagedAttentionPlan& plan, void* ws,
-                   const CascadePass& cp) {
+                   const LaunchExtras& cp) {
   const float scale = a->scale > 0.f ? a->scale : (float)(1.0 / sqrt((double)a->head_dim));
   if (plan.prefill) {
     // The suffix pass is planned on the split-context kernel, which alone
@@ -347,6 +379,8 @@ int launch_planned(const mvr_paged_attention_args* a, const mvr::PagedAttentionP
     f.state_o = cp.state_o;
     f.state_lse = cp.state_lse;
     f.state_tokens = cp.state_tokens;
+    f.class_q_min = cp.class_q_min;
+    f.class_q_max = cp.class_q_max;
     TraceRange launch("attn-prefill-fused");
     hipError_t err = mvr::launch_paged_prefill(f, a->head_dim, static_cast<hipStream_t>(a->stream));
     if (err != hipSuccess) return fail(MVR_E_HIP, "kernel launch failed: %s", hipGetErrorString(err));
@@ -387,6 +421,8 @@ int launch_planned(const mvr_paged_attention_args* a, const mvr::PagedAttentionP
   p.prefix_o = cp.prefix_o;
   p.prefix_lse = cp.prefix_lse;
   p.seq_prefix_len = cp.seq_prefix_len;
+  p.class_q_min = cp.class_q_min;
+  p.class_q_max = cp.class_q_max;
 
   TraceRange launch("attn-paged-fused"); // one launch replaces attn-qk / attn-mask-softmax / attn-paged-v
   hipError_t err = mvr::launch_paged_attention(plan, p, static_cast<hipStream_t>(a->stream));
@@ -402,6 +438,90 @@ int check_workspace(const mvr_paged_attention_args* a, size_t need) {
   return MVR_OK;
 }
 
+// One mvr_paged_attention call as one launch sequence, or two for a batch
+// that mixes decode-sized requests (grouped rows G * q_len <= kSmallRows: one
+// row tile of the split-context kernel) with prefill-sized ones.  Planned for
+// its longest query, such a call would give every decode sequence the prefill
+// kernel's 128-row tiles (or, in F32, 32-row split-context tiles with few
+// context partitions).  With a host copy of cu_q_lens the planner instead
+// launches each class over the range of sequences that holds it (pointers of
+// the tables offset to the range's first sequence), planned for that class
+// alone; a sequence of the other class inside the range has no rows there.
+// Each launch writes only its own sequences' rows of `out`.
+constexpr int kSmallRows = 32;
+
+struct CallPlan {
+  int n = 1;                       // launches (1 or 2)
+  mvr_paged_attention_args part[2]; // each launch's view of the call
+  mvr::PagedAttentionPlan plan[2];
+  LaunchExtras extras[2];
+  size_t offset[2] = {0, 0};       // workspace offset of each launch's partials
+  size_t total = 0;
+};
+
+CallPlan make_call_plan(const mvr_paged_attention_args* a) {
+  CallPlan c;
+  c.part[0] = *a;
+  c.plan[0] = make_plan(a);
+  c.total = c.plan[0].partial_bytes;
+  const int32_t* cu = a->cu_q_lens_host;
+  const int32_t* sl = a->seq_lens_host;
+  if (!cu || a->num_seqs < 2 || (int64_t)a->max_q_len * (a->num_q_heads / a->num_kv_heads) <= kSmallRows) return c;
+  const int group = a->num_q_heads / a->num_kv_heads;
+  int first[2] = {-1, -1}, last[2] = {-1, -1}, qmin[2] = {INT32_MAX, INT32_MAX}, qmax[2] = {0, 0}, lmax[2] = {0, 0};
+  int64_t lsum[2] = {0, 0};
+  for (int s = 0; s < a->num_seqs; s++) {
+    const int q = cu[s + 1] - cu[s];
+    const int L = sl ? sl[s] : a->max_seq_len;
+    // Hints that break the call's own bounds are not used (the device tables
+    // are what the kernels read; mvr_paged_attention_validate reports them).
+    if (q < 1 || q > a->max_q_len || L < q || L > a->max_seq_len) return c;
+    const int k = (int64_t)group * q <= kSmallRows ? 0 : 1;
+    if (first[k] < 0) first[k] = s;
+    last[k] = s;
+    qmin[k] = q < qmin[k] ? q : qmin[k];
+    qmax[k] = q > qmax[k] ? q : qmax[k];
+    lmax[k] = L > lmax[k] ? L : lmax[k];
+    lsum[k] += L;
+  }
+  if (first[0] < 0 || first[1] < 0) return c; // one class: one launch
+  c.n = 2;
+  size_t off = 0;
+  for (int k = 0; k < 2; k++) {
+    mvr_paged_attention_args& p = c.part[k];
+    p = *a;
+    const int f = first[k];
+    p.num_seqs = last[k] - f + 1;
+    // (null tables only when sizing a repacked call's workspace)
+    p.block_tables = a->block_tables ? a->block_tables + (int64_t)f * a->max_pages_per_seq : nullptr;
+    p.seq_lens = a->seq_lens ? a->seq_lens + f : nullptr;
+    p.cu_q_lens = a->cu_q_lens ? a->cu_q_lens + f : nullptr; // q_start stays the whole call's packed index
+    p.seq_lens_host = sl ? sl + f : nullptr;
+    p.cu_q_lens_host = cu + f;
+    p.max_q_len = qmax[k];
+    p.max_seq_len = sl ? lmax[k] : a->max_seq_len;
+    // The range may hold sequences of the other class (no rows here); the
+    // hint counts this class's keys only.
+    p.sum_seq_lens = sl ? lsum[k] : 0;
+    if (p.sum_seq_lens > (int64_t)p.max_seq_len * p.num_seqs) p.sum_seq_lens = 0;
+    c.plan[k] = make_plan(&p);
+    c.extras[k].class_q_min = qmin[k];
+    c.extras[k].class_q_max = qmax[k];
+    c.offset[k] = off;
+    off += align_up(c.plan[k].partial_bytes, 256);
+  }
+  c.total = c.offset[1] + c.plan[1].partial_bytes;
+  return c;
+}
+
+int launch_call(const CallPlan& c, char* ws) {
+  for (int k = 0; k < c.n; k++) {
+    const int rc = launch_planned(&c.part[k], c.plan[k], ws ? ws + c.offset[k] : nullptr, c.extras[k]);
+    if (rc != MVR_OK) return rc;
+  }
+  return MVR_OK;
+}
+
 // Page sizes that are not a multiple of 16 (the reference allows any
 // per_page_token_count; its own tests use 2 and 3): the kernels read whole
 // 16-token chunks of one page, so such a call first repacks every sequence's
@@ -412,7 +532,7 @@ int check_workspace(const mvr_paged_attention_args* a, size_t need) {
 // Workspace: [keys][values][block table][the plan's partials].
 struct RepackPlan {
   mvr_paged_attention_args a16; // the call on the repacked layout (pointers into the workspace)
-  mvr::PagedAttentionPlan plan;
+  CallPlan call;
   int pages16;
   size_t off_part, total;
 };
@@ -432,8 +552,8 @@ RepackPlan make_repack_plan(const mvr_paged_attention_args* a, char* ws) {
   r.a16.key_pool = ws;
   r.a16.value_pool = ws ? ws + off_v : nullptr;
   r.a16.block_tables = ws ? reinterpret_cast<const int32_t*>(ws + off_bt) : nullptr;
-  r.plan = make_plan(&r.a16);
-  r.total = r.off_part + r.plan.partial_bytes;
+  r.call = make_call_plan(&r.a16);
+  r.total = r.off_part + r.call.total;
   return r;
 }
 
@@ -556,10 +676,24 @@ static int check_rope_append(const mvr_rope_append_args* a) {
 }
 
 int mvr_rope_append(const mvr_rope_append_args* a) {
-  TraceRange range("attn-cache"); // trace.rs: attention_cache_append
+  // The reference traces forward_rope of the query and the key (trace.rs:77-79,
+  // common.rs:306-307, 351) and then the cache append (trace.rs:81-83,
+  // common.rs:310); here one launch does all three, so the append range
+  // (around the launch) sits inside the rope range.
+  TraceRange range("attn-rope tensor=query,key");
   g_last_error[0] = 0;
   int rc = check_rope_append(a);
   if (rc != MVR_OK) return rc;
+  if (checked_mode()) {
+    hipStream_t st = static_cast<hipStream_t>(a->stream);
+    std::vector<int32_t> bt, sl, cu;
+    if (!copy_table(a->block_tables, (size_t)a->num_seqs * a->max_pages_per_seq, st, bt) ||
+        !copy_table(a->seq_lens, (size_t)a->num_seqs, st, sl) || !copy_table(a->cu_q_lens, (size_t)a->num_seqs + 1, st, cu))
+      return fail(MVR_E_HIP, "checked mode: copying the device tables to the host failed");
+    rc = mvr_rope_append_validate(a, ptr_or_null(bt), ptr_or_null(sl), ptr_or_null(cu), nullptr);
+    if (rc != MVR_OK) return rc;
+  }
+  TraceRange append("attn-cache operation=append");
   mvr::RopeAppendParams p{};
   p.q = a->q;
   p.q_stride_head = a->q_stride_head;
@@ -656,7 +790,19 @@ int mvr_rope_append_validate(const mvr_rope_append_args* a, const int32_t* block
 size_t mvr_paged_attention_workspace_size(const mvr_paged_attention_args* args) {
   if (check_scalars(args) != MVR_OK) return 0;
   if (args->page_size % mvr::kChunkTokens != 0) return make_repack_plan(args, nullptr).total;
-  return make_plan(args).partial_bytes;
+  return make_call_plan(args).total;
+}
+
+// MVR_ATTN_CHECKED: the device tables of an attention call through
+// mvr_paged_attention_validate.
+static int checked_attention_tables(const mvr_paged_attention_args* a) {
+  hipStream_t st = static_cast<hipStream_t>(a->stream);
+  std::vector<int32_t> bt, sl, cu;
+  if (!copy_table(a->block_tables, (size_t)a->num_seqs * a->max_pages_per_seq, st, bt) ||
+      !copy_table(a->seq_lens, (size_t)a->num_seqs, st, sl) ||
+      !copy_table(a->cu_q_lens, (size_t)a->num_seqs + 1, st, cu))
+    return fail(MVR_E_HIP, "checked mode: copying the device tables to the host failed");
+  return mvr_paged_attention_validate(a, ptr_or_null(bt), ptr_or_null(sl), ptr_or_null(cu));
 }
 
 int mvr_paged_attention(const mvr_paged_attention_args* a) {
@@ -664,22 +810,24 @@ int mvr_paged_attention(const mvr_paged_attention_args* a) {
   g_last_error[0] = 0;
   int rc = check_scalars(a);
   if (rc != MVR_OK) return rc;
+  if (checked_mode() && (rc = checked_attention_tables(a)) != MVR_OK) return rc;
   if (a->page_size % mvr::kChunkTokens != 0) {
     const RepackPlan r = make_repack_plan(a, static_cast<char*>(a->workspace));
     rc = check_workspace(a, r.total);
     if (rc != MVR_OK) return rc;
     const int es = a->dtype == MVR_DTYPE_F16 ? 2 : 4;
+    TraceRange repack("attn-cache operation=access result_layout=repacked");
     hipError_t err = mvr::launch_repack_pages(
         a->key_pool, a->value_pool, a->block_tables, a->max_pages_per_seq, a->seq_lens, a->max_seq_len, a->num_seqs,
         a->num_kv_heads, a->page_size, a->head_dim, es, r.pages16, const_cast<void*>(r.a16.key_pool),
         const_cast<void*>(r.a16.value_pool), const_cast<int32_t*>(r.a16.block_tables), static_cast<hipStream_t>(a->stream));
     if (err != hipSuccess) return fail(MVR_E_HIP, "kernel launch failed: %s", hipGetErrorString(err));
-    return launch_planned(&r.a16, r.plan, static_cast<char*>(a->workspace) + r.off_part, CascadePass());
+    return launch_call(r.call, static_cast<char*>(a->workspace) + r.off_part);
   }
-  const mvr::PagedAttentionPlan plan = make_plan(a);
-  rc = check_workspace(a, plan.partial_bytes);
+  const CallPlan c = make_call_plan(a);
+  rc = check_workspace(a, c.total);
   if (rc != MVR_OK) return rc;
-  return launch_planned(a, plan, a->workspace, CascadePass());
+  return launch_call(c, static_cast<char*>(a->workspace));
 }
 
 size_t mvr_paged_attention_cascade_workspace_size(const mvr_paged_attention_args* args,
@@ -693,6 +841,22 @@ int mvr_paged_attention_cascade(const mvr_paged_attention_args* a, const mvr_cas
   g_last_error[0] = 0;
   int rc = check_cascade(a, g);
   if (rc != MVR_OK) return rc;
+  if (checked_mode()) {
+    hipStream_t st = static_cast<hipStream_t>(a->stream);
+    const size_t ng = g->num_groups > 0 ? (size_t)g->num_groups : 0;
+    std::vector<int32_t> bt, sl, cu, gcu, gpre, gbt, spre;
+    if (!copy_table(a->block_tables, (size_t)a->num_seqs * a->max_pages_per_seq, st, bt) ||
+        !copy_table(a->seq_lens, (size_t)a->num_seqs, st, sl) || !copy_table(a->cu_q_lens, (size_t)a->num_seqs + 1, st, cu) ||
+        !copy_table(ng ? g->group_cu_q_lens : nullptr, ng + 1, st, gcu) ||
+        !copy_table(ng ? g->group_prefix_lens : nullptr, ng, st, gpre) ||
+        !copy_table(ng ? g->group_block_tables : nullptr, ng * a->max_pages_per_seq, st, gbt) ||
+        !copy_table(g->seq_prefix_lens, (size_t)a->num_seqs, st, spre))
+      return fail(MVR_E_HIP, "checked mode: copying the device tables to the host failed");
+    rc = mvr_paged_attention_cascade_validate(a, g, ptr_or_null(bt), ptr_or_null(sl), ptr_or_null(cu),
+                                              ptr_or_null(gcu), ptr_or_null(gpre), ptr_or_null(gbt),
+                                              ptr_or_null(spre));
+    if (rc != MVR_OK) return rc;
+  }
   const CascadePlan c = make_cascade_plan(a, g);
   rc = check_workspace(a, c.total);
   if (rc != MVR_OK) return rc;
@@ -700,7 +864,7 @@ int mvr_paged_attention_cascade(const mvr_paged_attention_args* a, const mvr_cas
   float* a_o = reinterpret_cast<float*>(ws + c.off_a_o);
   float* a_lse = reinterpret_cast<float*>(ws + c.off_a_lse);
   if (g->num_groups > 0) {
-    CascadePass pre;
+    LaunchExtras pre;
     pre.key_end = g->group_prefix_lens;
     pre.state_o = a_o;
     pre.state_lse = a_lse;
@@ -709,7 +873,7 @@ int mvr_paged_attention_cascade(const mvr_paged_attention_args* a, const mvr_cas
     if (rc != MVR_OK) return rc;
   }
   // The suffix pass writes `out`, each row merged with its prefix state.
-  CascadePass suf;
+  LaunchExtras suf;
   suf.key_begin = g->seq_prefix_lens;
   suf.state_tokens = c.state_tokens;
   if (g->num_groups > 0) {
@@ -865,7 +1029,8 @@ int mvr_forward_paged_attention(int32_t dtype, const mvr_attention_dimensions* d
 int mvr_reconstruct_contiguous(int32_t dtype, const void* pool, int64_t page_count, int32_t num_kv_heads,
                                int32_t per_page_token_count, int32_t head_dim, const int32_t* page_ids,
                                int32_t num_page_ids, int32_t cached_token_count, void* out, void* stream) {
-  TraceRange range("attn-cache"); // trace.rs:85, the access that materialises contiguous K/V
+  // trace.rs:85-92: the access that materialises contiguous K/V (common.rs:386)
+  TraceRange range("attn-cache operation=access result_layout=contiguous");
   g_last_error[0] = 0;
   if (dtype != MVR_DTYPE_F32 && dtype != MVR_DTYPE_F16)
     return fail(MVR_E_UNSUPPORTED, "dtype %d is not F32 (0) or F16 (1)", dtype);

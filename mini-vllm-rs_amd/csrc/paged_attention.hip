@@ -25,6 +25,8 @@
 
 #include <math.h>
 
+#include <atomic>
+
 namespace mvr {
 namespace {
 
@@ -62,7 +64,10 @@ struct SeqInfo {
 
 __device__ __forceinline__ SeqInfo load_seq(const PagedAttentionParams& p, int b) {
   SeqInfo s;
-  s.seq_len = p.seq_lens ? p.seq_lens[b] : p.single_seq_len;
+  // single_seq_len is the call's max_seq_len, whose pages the host has checked
+  // to fit a block-table row: a larger device seq_len (a broken contract) is
+  // clamped so that no read leaves the row or the planned partitions.
+  s.seq_len = p.seq_lens ? min(p.seq_lens[b], p.single_seq_len) : p.single_seq_len;
   if (p.cu_q_lens) {
     s.q_start = p.cu_q_lens[b];
     s.q_len = p.cu_q_lens[b + 1] - s.q_start;
@@ -70,6 +75,8 @@ __device__ __forceinline__ SeqInfo load_seq(const PagedAttentionParams& p, int b
     s.q_start = 0;
     s.q_len = p.single_q_len;
   }
+  // Another launch's sequence: no rows here (every unit of it exits at once).
+  if (s.q_len < p.class_q_min || (p.class_q_max > 0 && s.q_len > p.class_q_max)) s.q_len = 0;
   s.key_begin = p.key_begin ? p.key_begin[b] : 0;
   if (p.key_end) {
     s.key_end = p.key_end[b];
@@ -559,22 +566,25 @@ __global__ __launch_bounds__(kWaveSize* kWavesPerBlock, DEPTH == 3 ? 2 : Tr::tem
     __syncthreads();
     static_assert(kWavesPerBlock == 4, "the den sum below follows a 4-partition butterfly");
     constexpr int kPer = D / kWaveSize;
+    // At most one partition per wavefront holds a result (seq_len is clamped to
+    // max_seq_len, which the plan splits into exactly kWavesPerBlock parts).
+    const int n_held = min(n_parts, kWavesPerBlock);
     for (int rr = wave; rr < kTileRows; rr += kWavesPerBlock) {
       const int rho = rt * kTileRows + rr;
-      if (rho >= rows || n_parts == 0) continue;
+      if (rho >= rows || n_held == 0) continue;
       float mj[kWavesPerBlock], wl[kWavesPerBlock];
       float mmax = -INFINITY;
 #pragma unroll
       for (int j = 0; j < kWavesPerBlock; j++) {
-        mj[j] = j < n_parts ? merge_ml[(j * kTileRows + rr) * 2] : -INFINITY;
+        mj[j] = j < n_held ? merge_ml[(j * kTileRows + rr) * 2] : -INFINITY;
         mmax = fmaxf(mmax, mj[j]);
       }
       const float m_use = mmax == -INFINITY ? 0.f : mmax;
       float w[kWavesPerBlock];
 #pragma unroll
       for (int j = 0; j < kWavesPerBlock; j++) {
-        w[j] = j < n_parts ? __builtin_amdgcn_exp2f(mj[j] - m_use) : 0.f;
-        wl[j] = j < n_parts ? w[j] * merge_ml[(j * kTileRows + rr) * 2 + 1] : 0.f;
+        w[j] = j < n_held ? __builtin_amdgcn_exp2f(mj[j] - m_use) : 0.f;
+        wl[j] = j < n_held ? w[j] * merge_ml[(j * kTileRows + rr) * 2 + 1] : 0.f;
       }
       // merge_partitions_kernel sums lane j's w_j l_j over the wavefront by
       // xor-shuffles; with partitions in lanes 0..3 that is (0 + 2) + (1 + 3).
@@ -582,7 +592,7 @@ __global__ __launch_bounds__(kWaveSize* kWavesPerBlock, DEPTH == 3 ? 2 : Tr::tem
       float acc[kPer];
 #pragma unroll
       for (int e = 0; e < kPer; e++) acc[e] = 0.f;
-      for (int j = 0; j < n_parts; j++) {
+      for (int j = 0; j < n_held; j++) {
         const float* src = merge_o + (j * kTileRows + rr) * kMergeStride + l * kPer;
 #pragma unroll
         for (int e = 0; e < kPer; e++) acc[e] = fmaf(w[j], src[e], acc[e]);
@@ -818,13 +828,18 @@ namespace {
 
 template <typename Tr, int D, int NB>
 int64_t resident_waves_typed() {
-  // Cached per device; the query result never changes, so racing writers
-  // store the same value.
+  // Cached per device.  Threads driving several devices call this at once:
+  // the entries are atomics (relaxed: each is written once with a value that
+  // never changes, so racing writers store the same number and a reader sees
+  // either 0, and asks the runtime itself, or that number).
   constexpr int kMaxDevices = 64;
-  static int64_t cache[kMaxDevices] = {};
+  static std::atomic<int64_t> cache[kMaxDevices];
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0) return 0;
-  if (dev < kMaxDevices && cache[dev] > 0) return cache[dev];
+  if (dev < kMaxDevices) {
+    const int64_t known = cache[dev].load(std::memory_order_relaxed);
+    if (known > 0) return known;
+  }
   int cus = 0, blocks = 0;
   if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
       hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, paged_attention_kernel<Tr, D, NB>,
@@ -837,7 +852,7 @@ int64_t resident_waves_typed() {
   // with shorter ones (371 vs 395 us): less merge traffic, fewer streams
   // competing for the same DRAM rows.
   const int64_t waves = (int64_t)cus * (blocks < 2 ? blocks : 2) * kWavesPerBlock;
-  if (dev < kMaxDevices) cache[dev] = waves;
+  if (dev < kMaxDevices) cache[dev].store(waves, std::memory_order_relaxed);
   return waves;
 }
 

@@ -49,6 +49,11 @@ struct PagedAttentionParams {
   const float* prefix_o;          // [q head][state_tokens][D], normalised
   const float* prefix_lse;        // [q head][state_tokens], log2 units
   const int32_t* seq_prefix_len;  // [num_seqs]
+  // Sequences whose q_len lies outside [class_q_min, class_q_max] (0 = no
+  // upper bound) belong to another launch of the same call and are skipped:
+  // a batch mixing decode-sized and prefill-sized requests runs each class
+  // on a grid planned for it.
+  int32_t class_q_min, class_q_max;
 };
 
 // Grid shape chosen by the host.

@@ -94,7 +94,9 @@ __device__ __forceinline__ void tile_barrier() {
 
 __device__ __forceinline__ SeqRows load_rows(const PrefillParams& p, int b) {
   SeqRows s;
-  s.seq_len = p.seq_lens ? p.seq_lens[b] : p.single_seq_len;
+  // single_seq_len is the call's max_seq_len (its pages fit a block-table row,
+  // checked on the host): a larger device seq_len is clamped to it.
+  s.seq_len = p.seq_lens ? min(p.seq_lens[b], p.single_seq_len) : p.single_seq_len;
   if (p.cu_q_lens) {
     s.q_start = p.cu_q_lens[b];
     s.q_len = p.cu_q_lens[b + 1] - s.q_start;
@@ -102,6 +104,8 @@ __device__ __forceinline__ SeqRows load_rows(const PrefillParams& p, int b) {
     s.q_start = 0;
     s.q_len = p.single_q_len;
   }
+  // Another launch's sequence: no rows here (its blocks exit at once).
+  if (s.q_len < p.class_q_min || (p.class_q_max > 0 && s.q_len > p.class_q_max)) s.q_len = 0;
   if (p.key_end) { // cascade prefix pass: every row sees every key before key_end
     s.key_end = p.key_end[b];
     s.seq_len = s.key_end + s.q_len;

@@ -34,6 +34,9 @@ struct PrefillParams {
   float* state_o;   // [q head][state_tokens][D]
   float* state_lse; // [q head][state_tokens]
   int32_t state_tokens;
+  // Sequences with q_len outside [class_q_min, class_q_max] (0 = no upper
+  // bound) belong to another launch of the same call and are skipped.
+  int32_t class_q_min, class_q_max;
 };
 
 hipError_t launch_paged_prefill(const PrefillParams& params, int head_dim, hipStream_t stream);

@@ -19,6 +19,7 @@ there is no CPU fallback, and a missing library raises.
 """
 from __future__ import annotations
 
+import contextlib
 import ctypes
 import math
 import os
@@ -27,6 +28,8 @@ from typing import Optional, Sequence
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libmvr_attn.so")
+
+ABI_VERSION = 2  # MVR_ATTN_ABI_VERSION of include/mvr_attn.h
 
 DTYPE_F32, DTYPE_F16 = 0, 1
 
@@ -94,6 +97,8 @@ class PagedAttentionArgs(ctypes.Structure):
         ("workspace_bytes", ctypes.c_size_t),
         ("stream", ctypes.c_void_p),
         ("sum_seq_lens", ctypes.c_int64),
+        ("seq_lens_host", ctypes.c_void_p),
+        ("cu_q_lens_host", ctypes.c_void_p),
     ]
 
 
@@ -217,8 +222,8 @@ def load_library():
     lib.mvr_paged_attention_cascade_validate.restype = ctypes.c_int
     lib.mvr_paged_attention_cascade_validate.argtypes = [ctypes.POINTER(PagedAttentionArgs),
                                                          ctypes.POINTER(CascadeGroups)] + [ctypes.c_void_p] * 7
-    if lib.mvr_abi_version() != 1:
-        raise RuntimeError("libmvr_attn.so ABI version mismatch")
+    if lib.mvr_abi_version() != ABI_VERSION:
+        raise RuntimeError(f"libmvr_attn.so ABI version {lib.mvr_abi_version()}, this binding is {ABI_VERSION}")
     _lib = lib
     return lib
 
@@ -251,10 +256,37 @@ def _stream_handle(stream) -> Optional[int]:
     return stream.cuda_stream
 
 
+def _stream_scope(stream, *tensors):
+    """Scope of one call launched on `stream`.  When that is not the current stream, the call's own
+    allocations (output, workspace) are made inside torch.cuda.stream(stream), so the caching allocator
+    hands their blocks to later work only in that stream's order, and every device tensor the kernels
+    read or write is recorded on `stream`, so that freeing it on its own stream before the kernels ran
+    cannot let another allocation reuse its memory meanwhile."""
+    torch = _torch()
+    if stream is None or stream == torch.cuda.current_stream():
+        return contextlib.nullcontext()
+    for t in tensors:
+        if t is not None and getattr(t, "is_cuda", False):
+            t.record_stream(stream)
+    return torch.cuda.stream(stream)
+
+
+def _host_int32(x):
+    """A contiguous int32 numpy copy of a host table (or None)."""
+    if x is None:
+        return None
+    import numpy as np
+
+    return np.ascontiguousarray(x, dtype=np.int32)
+
+
 def make_args(q, key_pool, value_pool, block_tables, seq_lens, cu_q_lens, out, *, max_q_len: int,
-              max_seq_len: int, scale: float = 0.0, stream=None, sum_seq_lens: int = 0) -> PagedAttentionArgs:
+              max_seq_len: int, scale: float = 0.0, stream=None, sum_seq_lens: int = 0, seq_lens_host=None,
+              cu_q_lens_host=None) -> PagedAttentionArgs:
     """Fills the C argument struct.  q / out: [Hq, total_q, D] (last dim contiguous);
-    pools: [num_pages, 1, Hkv, page_size, D]; block_tables int32 [num_seqs, max_pages]."""
+    pools: [num_pages, 1, Hkv, page_size, D]; block_tables int32 [num_seqs, max_pages].
+    seq_lens_host / cu_q_lens_host: optional host copies of the two length tables (planning hints: with them a
+    batch mixing decode-sized and prefill-sized requests runs each class on its own launch)."""
     n_pages, one, hkv, page_size, d = key_pool.shape
     if one != 1 or value_pool.shape != key_pool.shape:
         raise MvrError(MVR_E_INVALID_ARGUMENT, "pools must be [num_pages, 1, num_kv_heads, page_size, head_dim]")
@@ -287,9 +319,16 @@ def make_args(q, key_pool, value_pool, block_tables, seq_lens, cu_q_lens, out, *
     a.out_stride_token = out.stride(1)
     a.stream = _stream_handle(stream)
     a.sum_seq_lens = int(sum_seq_lens)
+    sl_h, cu_h = _host_int32(seq_lens_host), _host_int32(cu_q_lens_host)
+    if sl_h is not None and sl_h.shape != (a.num_seqs,):
+        raise MvrError(MVR_E_INVALID_ARGUMENT, "seq_lens_host must hold num_seqs entries")
+    if cu_h is not None and cu_h.shape != (a.num_seqs + 1,):
+        raise MvrError(MVR_E_INVALID_ARGUMENT, "cu_q_lens_host must hold num_seqs + 1 entries")
+    a.seq_lens_host = sl_h.ctypes.data if sl_h is not None else None
+    a.cu_q_lens_host = cu_h.ctypes.data if cu_h is not None else None
     # The struct holds raw device addresses: keep the tensors alive with it, so that a table built inline
     # (make_args(..., torch.tensor(...).cuda(), ...)) is not freed and its memory reused before the launch.
-    a._keep = (q, key_pool, value_pool, block_tables, seq_lens, cu_q_lens, out)
+    a._keep = (q, key_pool, value_pool, block_tables, seq_lens, cu_q_lens, out, sl_h, cu_h)
     return a
 
 
@@ -304,20 +343,23 @@ def new_workspace(nbytes: int, device):
 
 
 def paged_attention(q, key_pool, value_pool, block_tables, seq_lens, cu_q_lens, out=None, *, max_q_len: int,
-                    max_seq_len: int, scale: float = 0.0, workspace=None, stream=None, sum_seq_lens: int = 0):
+                    max_seq_len: int, scale: float = 0.0, workspace=None, stream=None, sum_seq_lens: int = 0,
+                    seq_lens_host=None, cu_q_lens_host=None):
     """Batched page-wise attention; returns out [Hq, total_q, D] in q's dtype."""
     torch = _torch()
-    if out is None:
-        out = torch.empty_like(q, memory_format=torch.contiguous_format)
-    a = make_args(q, key_pool, value_pool, block_tables, seq_lens, cu_q_lens, out, max_q_len=max_q_len,
-                  max_seq_len=max_seq_len, scale=scale, stream=stream, sum_seq_lens=sum_seq_lens)
-    need = workspace_size(a)
-    if need and (workspace is None or workspace.numel() * workspace.element_size() < need):
-        workspace = new_workspace(need, q.device)
-    if workspace is not None:
-        a.workspace = workspace.data_ptr()
-        a.workspace_bytes = workspace.numel() * workspace.element_size()
-    _check(load_library().mvr_paged_attention(ctypes.byref(a)))
+    with _stream_scope(stream, q, key_pool, value_pool, block_tables, seq_lens, cu_q_lens, out, workspace):
+        if out is None:
+            out = torch.empty_like(q, memory_format=torch.contiguous_format)
+        a = make_args(q, key_pool, value_pool, block_tables, seq_lens, cu_q_lens, out, max_q_len=max_q_len,
+                      max_seq_len=max_seq_len, scale=scale, stream=stream, sum_seq_lens=sum_seq_lens,
+                      seq_lens_host=seq_lens_host, cu_q_lens_host=cu_q_lens_host)
+        need = workspace_size(a)
+        if need and (workspace is None or workspace.numel() * workspace.element_size() < need):
+            workspace = new_workspace(need, q.device)
+        if workspace is not None:
+            a.workspace = workspace.data_ptr()
+            a.workspace_bytes = workspace.numel() * workspace.element_size()
+        _check(load_library().mvr_paged_attention(ctypes.byref(a)))
     return out
 
 
@@ -356,14 +398,15 @@ def forward_paged_attention(request_q, layout: PagedCacheLayout, num_q_heads: in
     c = PagedCacheLayoutC(layout.key_pool.data_ptr(), layout.value_pool.data_ptr(), layout.key_pool.shape[0],
                           layout.page_ids.data_ptr(), layout.page_ids.numel(), layout.per_page_token_count,
                           layout.cached_token_count)
-    q = request_q.contiguous()
-    y = torch.empty_like(q)
-    dt = dtype_code(q)
-    lib = load_library()
-    need = int(lib.mvr_forward_paged_attention_workspace_size(dt, ctypes.byref(dims), ctypes.byref(c)))
-    ws = new_workspace(need, q.device)
-    _check(lib.mvr_forward_paged_attention(dt, ctypes.byref(dims), ctypes.byref(c), q.data_ptr(), y.data_ptr(),
-                                           ws.data_ptr(), need, _stream_handle(stream)))
+    with _stream_scope(stream, request_q, layout.key_pool, layout.value_pool, layout.page_ids):
+        q = request_q.contiguous()
+        y = torch.empty_like(q)
+        dt = dtype_code(q)
+        lib = load_library()
+        need = int(lib.mvr_forward_paged_attention_workspace_size(dt, ctypes.byref(dims), ctypes.byref(c)))
+        ws = new_workspace(need, q.device)
+        _check(lib.mvr_forward_paged_attention(dt, ctypes.byref(dims), ctypes.byref(c), q.data_ptr(), y.data_ptr(),
+                                               ws.data_ptr(), need, _stream_handle(stream)))
     return y
 
 
@@ -372,10 +415,11 @@ def reconstruct_contiguous(pool, page_ids, cached_token_count: int, stream=None)
     -> [1, Hkv, cached_token_count, D], bit-exact."""
     torch = _torch()
     n, _, hkv, page_size, d = pool.shape
-    out = torch.empty((1, hkv, max(int(cached_token_count), 0), d), dtype=pool.dtype, device=pool.device)
-    rc = load_library().mvr_reconstruct_contiguous(dtype_code(pool), pool.data_ptr(), n, hkv, page_size, d,
-                                                   page_ids.data_ptr(), page_ids.numel(), int(cached_token_count),
-                                                   out.data_ptr(), _stream_handle(stream))
+    with _stream_scope(stream, pool, page_ids):
+        out = torch.empty((1, hkv, max(int(cached_token_count), 0), d), dtype=pool.dtype, device=pool.device)
+        rc = load_library().mvr_reconstruct_contiguous(dtype_code(pool), pool.data_ptr(), n, hkv, page_size, d,
+                                                       page_ids.data_ptr(), page_ids.numel(), int(cached_token_count),
+                                                       out.data_ptr(), _stream_handle(stream))
     _check(rc)
     return out
 
@@ -431,11 +475,13 @@ def rope_append(q, k, v, cos_table, sin_table, block_tables, seq_lens, cu_q_lens
     """Rotates q into q_out (a new tensor unless given; may be q itself) and writes the rotated k and v into
     their page slots; returns q_out."""
     torch = _torch()
-    if q_out is None:
-        q_out = torch.empty_like(q, memory_format=torch.contiguous_format)
-    a = make_rope_append_args(q, k, v, cos_table, sin_table, block_tables, seq_lens, cu_q_lens, key_pool, value_pool,
-                              q_out, max_seq_len=max_seq_len, rope_type=rope_type, stream=stream)
-    _check(load_library().mvr_rope_append(ctypes.byref(a)))
+    with _stream_scope(stream, q, k, v, cos_table, sin_table, block_tables, seq_lens, cu_q_lens, key_pool,
+                       value_pool, q_out):
+        if q_out is None:
+            q_out = torch.empty_like(q, memory_format=torch.contiguous_format)
+        a = make_rope_append_args(q, k, v, cos_table, sin_table, block_tables, seq_lens, cu_q_lens, key_pool,
+                                  value_pool, q_out, max_seq_len=max_seq_len, rope_type=rope_type, stream=stream)
+        _check(load_library().mvr_rope_append(ctypes.byref(a)))
     return q_out
 
 
@@ -481,19 +527,21 @@ def paged_attention_cascade(q, key_pool, value_pool, block_tables, seq_lens, cu_
                             stream=None, sum_seq_lens: int = 0):
     """paged_attention with each group's shared prefix attended once; returns out [Hq, total_q, D]."""
     torch = _torch()
-    if out is None:
-        out = torch.empty_like(q, memory_format=torch.contiguous_format)
-    a = make_args(q, key_pool, value_pool, block_tables, seq_lens, cu_q_lens, out, max_q_len=max_q_len,
-                  max_seq_len=max_seq_len, scale=scale, stream=stream, sum_seq_lens=sum_seq_lens)
-    lib = load_library()
-    need = int(lib.mvr_paged_attention_cascade_workspace_size(ctypes.byref(a), ctypes.byref(groups)))
-    if need == 0:
-        _check(lib.mvr_paged_attention_cascade(ctypes.byref(a), ctypes.byref(groups)))  # raises with the reason
-    if workspace is None or workspace.numel() * workspace.element_size() < need:
-        workspace = new_workspace(need, q.device)
-    a.workspace = workspace.data_ptr()
-    a.workspace_bytes = workspace.numel() * workspace.element_size()
-    _check(lib.mvr_paged_attention_cascade(ctypes.byref(a), ctypes.byref(groups)))
+    with _stream_scope(stream, q, key_pool, value_pool, block_tables, seq_lens, cu_q_lens, out, workspace,
+                       *groups._keep):
+        if out is None:
+            out = torch.empty_like(q, memory_format=torch.contiguous_format)
+        a = make_args(q, key_pool, value_pool, block_tables, seq_lens, cu_q_lens, out, max_q_len=max_q_len,
+                      max_seq_len=max_seq_len, scale=scale, stream=stream, sum_seq_lens=sum_seq_lens)
+        lib = load_library()
+        need = int(lib.mvr_paged_attention_cascade_workspace_size(ctypes.byref(a), ctypes.byref(groups)))
+        if need == 0:
+            _check(lib.mvr_paged_attention_cascade(ctypes.byref(a), ctypes.byref(groups)))  # raises with the reason
+        if workspace is None or workspace.numel() * workspace.element_size() < need:
+            workspace = new_workspace(need, q.device)
+        a.workspace = workspace.data_ptr()
+        a.workspace_bytes = workspace.numel() * workspace.element_size()
+        _check(lib.mvr_paged_attention_cascade(ctypes.byref(a), ctypes.byref(groups)))
     return out
 
 

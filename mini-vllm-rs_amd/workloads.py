@@ -135,26 +135,44 @@ def qwen2_05b_batched_decode_f16() -> Workload:
                     np.ones(8, np.int32), bt, seed)
 
 
-def llama3_8b_decode_b64_8k_f16(batch: int = 64) -> Workload:
-    """Batch 64 x 8192 tokens, 32 Q / 8 KV, D 128, pool = exact fit (32768 pages), permuted."""
+def llama3_8b_decode_b64_8k_f16(batch: int = 64, dtype: str = "f16") -> Workload:
+    """Batch 64 x 8192 tokens, 32 Q / 8 KV, D 128, pool = exact fit (32768 pages), permuted.  dtype "f32" gives the
+    same shape in F32, the activation dtype the reference's GPU backends force (server/mod.rs:505-530)."""
     seed = SEED_BASE + 3
     rng = np.random.default_rng(seed)
     seq_lens = np.full(batch, 8192, np.int32)
     num_pages = batch * 512
     bt = _assign_pages(rng, seq_lens, 16, num_pages)
-    return Workload(f"llama3-8b decode f16 b{batch} ctx8192", "f16", 32, 8, 128, 16, num_pages, 0.3, seq_lens,
+    return Workload(f"llama3-8b decode {dtype} b{batch} ctx8192", dtype, 32, 8, 128, 16, num_pages, 0.3, seq_lens,
                     np.ones(batch, np.int32), bt, seed)
 
 
-def qwen2_7b_chunked_prefill_f16() -> Workload:
-    """4 sequences, 2048 cached + 256 new tokens, 28 Q / 4 KV, D 128, pages in random order."""
+def qwen2_7b_chunked_prefill_f16(dtype: str = "f16") -> Workload:
+    """4 sequences, 2048 cached + 256 new tokens, 28 Q / 4 KV, D 128, pages in random order (dtype "f32": the same
+    shape in F32)."""
     seed = SEED_BASE + 4
     rng = np.random.default_rng(seed)
     seq_lens = np.full(4, 2048 + 256, np.int32)
     num_pages = 4 * math.ceil(2304 / 16)
     bt = _assign_pages(rng, seq_lens, 16, num_pages)
-    return Workload("qwen2-7b chunked prefill f16 b4 2048+256", "f16", 28, 4, 128, 16, num_pages, 0.3, seq_lens,
+    return Workload(f"qwen2-7b chunked prefill {dtype} b4 2048+256", dtype, 28, 4, 128, 16, num_pages, 0.3, seq_lens,
                     np.full(4, 256, np.int32), bt, seed)
+
+
+def llama3_8b_mixed_decode_prefill_f16(num_decode: int = 63, decode_ctx: int = 8192, prefix: int = 2048,
+                                       chunk: int = 256, dtype: str = "f16") -> Workload:
+    """The batch one scheduler step emits (scheduler.rs:258-271): the decode requests first, one token each,
+    then the prefill chunk that the remaining token budget admits.  Llama-3-8B shape (32 Q / 8 KV, D 128):
+    63 decodes over 8192 cached tokens and one 256-token chunk on a 2048-token cached prefix, 16-token pages
+    in random order."""
+    seed = SEED_BASE + 7
+    rng = np.random.default_rng(seed)
+    seq_lens = np.array([decode_ctx + 1] * num_decode + [prefix + chunk], np.int32)
+    q_lens = np.array([1] * num_decode + [chunk], np.int32)
+    num_pages = int(sum(math.ceil(int(L) / 16) for L in seq_lens))
+    bt = _assign_pages(rng, seq_lens, 16, num_pages)
+    return Workload(f"llama3-8b mixed {dtype} {num_decode} decodes ctx{decode_ctx} + prefill {prefix}+{chunk}", dtype,
+                    32, 8, 128, 16, num_pages, 0.3, seq_lens, q_lens, bt, seed)
 
 
 def llama3_8b_spec_verify_f16() -> Workload:

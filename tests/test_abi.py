@@ -30,7 +30,7 @@ def test_library_exports_every_declared_symbol():
     out = subprocess.run(["nm", "-D", "--defined-only", M.library_path()], capture_output=True, text=True, check=True)
     exported = set(re.findall(r"\bT (mvr_[a-z0-9_]+)$", out.stdout, flags=re.M))
     assert set(declared) <= exported
-    assert M.load_library().mvr_abi_version() == 1
+    assert M.load_library().mvr_abi_version() == M.ABI_VERSION == 2
 
 
 def test_product_library_does_not_link_the_oracle():
