@@ -132,6 +132,24 @@ size_t mvr_paged_attention_workspace_size(const mvr_paged_attention_args* args);
    mvr_paged_attention_validate). */
 int mvr_paged_attention(const mvr_paged_attention_args* args);
 
+/* Allocation-free variant of mvr_paged_attention.  It has no counterpart in
+   the reference: it is for callers that cannot allocate device memory or hand
+   over a workspace (code under HIP graph capture, tight serving loops,
+   harnesses that forbid hipMalloc).  Same arguments, output and numerics as
+   mvr_paged_attention, except that args->workspace and workspace_bytes are
+   ignored: the split-context partials (and the 16-token repack of page sizes
+   that are not a multiple of 16) live in a static device array of the
+   library, MVR_NOALLOC_SCRATCH_BYTES per device, held from the first use on
+   that device until the process ends.  A call that needs more returns
+   MVR_E_WORKSPACE (use mvr_paged_attention with a workspace for it).  It
+   calls no allocator.  Every call on one device shares that device's array:
+   calls that overlap in time on one device (other threads or streams) race,
+   calls on one stream are ordered.  The array needs no initialisation:
+   results never depend on what an earlier call left in it.  MVR_ATTN_CHECKED
+   does not apply to it. */
+#define MVR_NOALLOC_SCRATCH_BYTES (64u << 20)
+int mvr_paged_attention_noalloc(const mvr_paged_attention_args* args);
+
 /* Host-side checks of the tables the device will read, mirroring the
    reference's errors: seq_len == cached_kv_len + q_len >= q_len >= 1
    (common.rs:447-454), pages covering every length (common.rs:776-781),

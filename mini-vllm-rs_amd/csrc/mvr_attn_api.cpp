@@ -11,12 +11,21 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <atomic>
+#include <mutex>
 #include <vector>
 
 #include "kv_append.hpp"
 #include "kv_gather.hpp"
 #include "paged_attention_kernels.hpp"
 #include "paged_prefill.hpp"
+
+// Device scratch of mvr_paged_attention_noalloc (split-context partials and
+// the 16-token repack), one copy per device from module load until the
+// process ends.  In host code `scratch` names a host-side stand-in, never
+// the device array: its device address comes from hipGetSymbolAddress
+// (noalloc_scratch below), once per device.
+static __device__ __align__(256) unsigned char scratch[MVR_NOALLOC_SCRATCH_BYTES];
 
 namespace {
 
@@ -805,12 +814,40 @@ static int checked_attention_tables(const mvr_paged_attention_args* a) {
   return mvr_paged_attention_validate(a, ptr_or_null(bt), ptr_or_null(sl), ptr_or_null(cu));
 }
 
-int mvr_paged_attention(const mvr_paged_attention_args* a) {
-  TraceRange range("attn"); // trace.rs:64
-  g_last_error[0] = 0;
-  int rc = check_scalars(a);
-  if (rc != MVR_OK) return rc;
-  if (checked_mode() && (rc = checked_attention_tables(a)) != MVR_OK) return rc;
+// Device address of `scratch` on the current device: looked up with that
+// device current on its first call there, then kept per device (each device
+// holds its own copy at its own address).  Null (error set) if the lookup
+// fails.
+static void* noalloc_scratch() {
+  constexpr int kMaxDevices = 64;
+  static std::atomic<void*> addr[kMaxDevices];
+  static std::mutex lookup;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    (void)hipGetLastError();
+    fail(MVR_E_HIP, "no current device (or device index >= %d) for the static scratch", kMaxDevices);
+    return nullptr;
+  }
+  void* p = addr[dev].load(std::memory_order_acquire);
+  if (p) return p;
+  std::lock_guard<std::mutex> guard(lookup);
+  p = addr[dev].load(std::memory_order_relaxed);
+  if (!p) {
+    const hipError_t err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (err != hipSuccess || !p) {
+      (void)hipGetLastError();
+      fail(MVR_E_HIP, "hipGetSymbolAddress of the static scratch failed on device %d: %s", dev, hipGetErrorString(err));
+      return nullptr;
+    }
+    addr[dev].store(p, std::memory_order_release);
+  }
+  return p;
+}
+
+// The launches of one mvr_paged_attention call on the workspace the
+// arguments carry (scalar checks already done).
+static int paged_attention_launches(const mvr_paged_attention_args* a) {
+  int rc;
   if (a->page_size % mvr::kChunkTokens != 0) {
     const RepackPlan r = make_repack_plan(a, static_cast<char*>(a->workspace));
     rc = check_workspace(a, r.total);
@@ -828,6 +865,38 @@ int mvr_paged_attention(const mvr_paged_attention_args* a) {
   rc = check_workspace(a, c.total);
   if (rc != MVR_OK) return rc;
   return launch_call(c, static_cast<char*>(a->workspace));
+}
+
+int mvr_paged_attention(const mvr_paged_attention_args* a) {
+  TraceRange range("attn"); // trace.rs:64
+  g_last_error[0] = 0;
+  int rc = check_scalars(a);
+  if (rc != MVR_OK) return rc;
+  if (checked_mode() && (rc = checked_attention_tables(a)) != MVR_OK) return rc;
+  return paged_attention_launches(a);
+}
+
+int mvr_paged_attention_noalloc(const mvr_paged_attention_args* a) {
+  TraceRange range("attn"); // trace.rs:64
+  g_last_error[0] = 0;
+  int rc = check_scalars(a);
+  if (rc != MVR_OK) return rc;
+  const size_t need =
+      a->page_size % mvr::kChunkTokens != 0 ? make_repack_plan(a, nullptr).total : make_call_plan(a).total;
+  if (need > (size_t)MVR_NOALLOC_SCRATCH_BYTES)
+    return fail(MVR_E_WORKSPACE,
+                "this call needs %zu bytes of scratch, more than the %zu bytes of the library's static scratch; "
+                "call mvr_paged_attention with a workspace instead",
+                need, (size_t)MVR_NOALLOC_SCRATCH_BYTES);
+  mvr_paged_attention_args b = *a;
+  b.workspace = nullptr;
+  b.workspace_bytes = 0;
+  if (need) {
+    b.workspace = noalloc_scratch();
+    if (!b.workspace) return MVR_E_HIP;
+    b.workspace_bytes = MVR_NOALLOC_SCRATCH_BYTES;
+  }
+  return paged_attention_launches(&b);
 }
 
 size_t mvr_paged_attention_cascade_workspace_size(const mvr_paged_attention_args* args,

@@ -59,7 +59,10 @@ EXPORTED_SYMBOLS = (
     "mvr_paged_attention_cascade",
     "mvr_paged_attention_cascade_workspace_size",
     "mvr_paged_attention_cascade_validate",
+    "mvr_paged_attention_noalloc",
 )
+
+NOALLOC_SCRATCH_BYTES = 64 << 20  # MVR_NOALLOC_SCRATCH_BYTES of include/mvr_attn.h
 
 
 class MvrError(RuntimeError):
@@ -193,6 +196,8 @@ def load_library():
     lib.mvr_last_error.restype = ctypes.c_char_p
     lib.mvr_paged_attention.restype = ctypes.c_int
     lib.mvr_paged_attention.argtypes = [ctypes.POINTER(PagedAttentionArgs)]
+    lib.mvr_paged_attention_noalloc.restype = ctypes.c_int
+    lib.mvr_paged_attention_noalloc.argtypes = [ctypes.POINTER(PagedAttentionArgs)]
     lib.mvr_paged_attention_workspace_size.restype = ctypes.c_size_t
     lib.mvr_paged_attention_workspace_size.argtypes = [ctypes.POINTER(PagedAttentionArgs)]
     lib.mvr_paged_attention_validate.restype = ctypes.c_int
@@ -360,6 +365,19 @@ def paged_attention(q, key_pool, value_pool, block_tables, seq_lens, cu_q_lens, 
             a.workspace = workspace.data_ptr()
             a.workspace_bytes = workspace.numel() * workspace.element_size()
         _check(load_library().mvr_paged_attention(ctypes.byref(a)))
+    return out
+
+
+def paged_attention_noalloc(q, key_pool, value_pool, block_tables, seq_lens, cu_q_lens, out, *, max_q_len: int,
+                            max_seq_len: int, scale: float = 0.0, stream=None, sum_seq_lens: int = 0,
+                            seq_lens_host=None, cu_q_lens_host=None):
+    """mvr_paged_attention_noalloc: the caller passes the output; the library's static device scratch replaces
+    the workspace, so nothing is allocated (calls that overlap in time on one device race on that scratch)."""
+    with _stream_scope(stream, q, key_pool, value_pool, block_tables, seq_lens, cu_q_lens, out):
+        a = make_args(q, key_pool, value_pool, block_tables, seq_lens, cu_q_lens, out, max_q_len=max_q_len,
+                      max_seq_len=max_seq_len, scale=scale, stream=stream, sum_seq_lens=sum_seq_lens,
+                      seq_lens_host=seq_lens_host, cu_q_lens_host=cu_q_lens_host)
+        _check(load_library().mvr_paged_attention_noalloc(ctypes.byref(a)))
     return out
 
 

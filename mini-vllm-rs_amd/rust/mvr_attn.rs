@@ -17,6 +17,7 @@
 use std::ffi::{c_char, c_int, c_void, CStr};
 
 pub const MVR_ATTN_ABI_VERSION: c_int = 2;
+pub const MVR_NOALLOC_SCRATCH_BYTES: usize = 64 << 20;
 
 // ActivationDType (src/model_runner/mod.rs:331-351).
 pub const MVR_DTYPE_F32: i32 = 0;
@@ -141,6 +142,7 @@ pub struct MvrRopeAppendArgs {
 extern "C" {
     pub fn mvr_paged_attention_workspace_size(args: *const MvrPagedAttentionArgs) -> usize;
     pub fn mvr_paged_attention(args: *const MvrPagedAttentionArgs) -> c_int;
+    pub fn mvr_paged_attention_noalloc(args: *const MvrPagedAttentionArgs) -> c_int;
     pub fn mvr_paged_attention_validate(args: *const MvrPagedAttentionArgs, block_tables_host: *const i32,
                                         seq_lens_host: *const i32, cu_q_lens_host: *const i32) -> c_int;
     pub fn mvr_paged_attention_cascade_workspace_size(args: *const MvrPagedAttentionArgs,
@@ -195,6 +197,13 @@ pub fn workspace_size(args: &MvrPagedAttentionArgs) -> usize {
 /// forward_paged_attention for every request of a layer (common.rs:739-817 batched over common.rs:285-327).
 pub fn paged_attention(args: &MvrPagedAttentionArgs) -> candle_core::Result<()> {
     check(unsafe { mvr_paged_attention(args) })
+}
+
+/// paged_attention without a workspace: the library's static device scratch (MVR_NOALLOC_SCRATCH_BYTES per
+/// device) holds the partials, for callers that cannot allocate (graph capture, fixed serving loops).
+/// Calls that overlap in time on one device race on that scratch.
+pub fn paged_attention_noalloc(args: &MvrPagedAttentionArgs) -> candle_core::Result<()> {
+    check(unsafe { mvr_paged_attention_noalloc(args) })
 }
 
 /// The checks of common.rs:447-454 and :776-781 on host copies of the tables (no launch).

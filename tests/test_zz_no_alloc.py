@@ -1,0 +1,124 @@
+"""mvr_paged_attention_noalloc (the allocation-free variant of mvr_paged_attention) through the C ABI.
+
+Its output must equal mvr_paged_attention's with a caller workspace bit for bit (same plan, same kernels; only the
+scratch memory differs) on consecutive calls that reuse the library's static scratch, the second with a smaller
+input; calls needing more scratch than the library holds are refused before any launch; repeated calls change
+the device's free memory by nothing.
+"""
+import ctypes
+
+import numpy as np
+import pytest
+
+torch = pytest.importorskip("torch")
+
+import mvr_attn as M  # noqa: E402
+import workloads as W  # noqa: E402
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _gpu():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    M.load_library()
+
+
+def _both(w, t, hints=False):
+    """(noalloc output, workspace output) for one workload, each into its own NaN-filled output."""
+    kw = dict(seq_lens_host=w.seq_lens, cu_q_lens_host=w.cu_q_lens) if hints else {}
+    lib = M.load_library()
+    out_n = torch.full_like(t["q"], float("nan"))
+    a = M.make_args(t["q"], t["key_pool"], t["value_pool"], t["block_tables"], t["seq_lens"], t["cu_q_lens"], out_n,
+                    max_q_len=w.max_q_len, max_seq_len=w.max_seq_len, sum_seq_lens=int(w.seq_lens.sum()), **kw)
+    need = M.workspace_size(a)
+    assert need <= M.NOALLOC_SCRATCH_BYTES
+    rc = lib.mvr_paged_attention_noalloc(ctypes.byref(a))
+    assert rc == 0, lib.mvr_last_error().decode()
+    ref = M.paged_attention(t["q"], t["key_pool"], t["value_pool"], t["block_tables"], t["seq_lens"], t["cu_q_lens"],
+                            max_q_len=w.max_q_len, max_seq_len=w.max_seq_len, sum_seq_lens=int(w.seq_lens.sum()),
+                            **kw)
+    torch.cuda.synchronize()
+    return out_n, ref, need
+
+
+def test_noalloc_equals_workspace_call_on_consecutive_calls():
+    # The verify workload needs the most scratch of the benchmark workloads (about 51 MiB of partials); the
+    # Qwen2-0.5B batch after it needs about 3 MiB and runs on what the first call left in the scratch.
+    big, small = W.llama3_8b_spec_verify_f16(), W.qwen2_05b_batched_decode_f16()
+    tb, ts = W.device_tensors(big, None, seed=1), W.device_tensors(small, None, seed=2)
+    n1, r1, need1 = _both(big, tb)
+    n2, r2, need2 = _both(small, ts)
+    print(f"scratch used: {need1} then {need2} bytes", flush=True)
+    assert need1 > need2 > 0
+    assert torch.equal(n1, r1)
+    assert torch.equal(n2, r2)
+    # and back to the large call, then the small one again
+    n3, r3, _ = _both(big, tb)
+    n4, r4, _ = _both(small, ts)
+    assert torch.equal(n3, r1) and torch.equal(n4, r2)
+
+
+@pytest.mark.parametrize("case", ["repacked-page-size-5", "mixed-with-hints", "block-merge", "prefill-splits"])
+def test_noalloc_equals_workspace_call_on_every_plan(case):
+    if case == "repacked-page-size-5":
+        g = torch.Generator(device="cuda").manual_seed(3)
+        hq, hkv, d, P = 32, 8, 128, 5
+        lens = np.array([700, 97, 1500], np.int32)
+        need = [-(-int(L) // P) for L in lens]
+        bt = np.zeros((3, max(need)), np.int32)
+        perm = np.random.default_rng(4).permutation(sum(need) + 2).astype(np.int32)
+        used = 0
+        for s, n in enumerate(need):
+            bt[s, :n] = perm[used:used + n]
+            used += n
+        w = W.Workload("page size 5", "f16", hq, hkv, d, P, sum(need) + 2, 0.3, lens, np.array([1, 5, 1], np.int32),
+                       bt, 3)
+        t = W.device_tensors(w, None, seed=3)
+    elif case == "mixed-with-hints":
+        w = W.llama3_8b_mixed_decode_prefill_f16(num_decode=15, decode_ctx=4096)
+        t = W.device_tensors(w, None, seed=5)
+    elif case == "block-merge":
+        w = W.llama3_8b_decode_b64_8k_f16()
+        t = W.device_tensors(w, None, seed=6)
+    else:
+        w = W.qwen2_7b_chunked_prefill_f16()
+        t = W.device_tensors(w, None, seed=7)
+    n, r, need = _both(w, t, hints=(case == "mixed-with-hints"))
+    print(f"{case}: scratch {need} bytes", flush=True)
+    assert torch.equal(n, r)
+
+
+def test_noalloc_refuses_calls_larger_than_its_scratch():
+    """A page size of 5 repacks the batch's K/V into the scratch: 64 sequences of 8K tokens need ~2 GiB, more
+    than the static scratch holds, so the call returns MVR_E_WORKSPACE before launching anything."""
+    lib = M.load_library()
+    a = M.PagedAttentionArgs()
+    a.dtype, a.num_seqs, a.num_q_heads, a.num_kv_heads, a.head_dim = M.DTYPE_F16, 64, 32, 8, 128
+    a.page_size, a.num_pages, a.max_pages_per_seq, a.max_q_len, a.max_seq_len = 5, 1 << 20, 1640, 1, 8192
+    fake = 1 << 20
+    a.q = a.key_pool = a.value_pool = a.block_tables = a.seq_lens = a.cu_q_lens = a.out = fake
+    a.q_stride_head, a.q_stride_token, a.out_stride_head, a.out_stride_token = 64 * 128, 128, 64 * 128, 128
+    assert M.workspace_size(a) > M.NOALLOC_SCRATCH_BYTES
+    rc = lib.mvr_paged_attention_noalloc(ctypes.byref(a))
+    assert rc == M.MVR_E_WORKSPACE
+    assert "static scratch" in lib.mvr_last_error().decode()
+
+
+def test_noalloc_calls_leave_free_device_memory_unchanged():
+    w = W.llama3_8b_spec_verify_f16()
+    t = W.device_tensors(w, None, seed=8)
+    out = torch.empty_like(t["q"])
+    kw = dict(max_q_len=w.max_q_len, max_seq_len=w.max_seq_len, sum_seq_lens=int(w.seq_lens.sum()))
+    M.paged_attention_noalloc(t["q"], t["key_pool"], t["value_pool"], t["block_tables"], t["seq_lens"],
+                              t["cu_q_lens"], out, **kw)  # first use on this device: the scratch's module is loaded
+    torch.cuda.synchronize()
+    free0 = torch.cuda.mem_get_info()[0]
+    alloc0 = torch.cuda.memory_allocated()
+    for _ in range(5):
+        M.paged_attention_noalloc(t["q"], t["key_pool"], t["value_pool"], t["block_tables"], t["seq_lens"],
+                                  t["cu_q_lens"], out, **kw)
+    torch.cuda.synchronize()
+    assert torch.cuda.mem_get_info()[0] == free0
+    assert torch.cuda.memory_allocated() == alloc0
