@@ -77,11 +77,22 @@ struct SeqRows {
 // bookkeeping of the direct-to-LDS loads stays exact; the empty asm
 // statements keep memory accesses from moving across the barrier without
 // any further wait.
-// 16 bytes per lane from global memory straight into LDS at lds + 16 * lane
-// (global_load_lds_dwordx4).  A plain __device__ function: lambdas in kernels
-// are also compiled for the host, where this gfx950 builtin does not exist.
-__device__ __forceinline__ void load_to_lds16(const void* src, void* lds) {
-  __builtin_amdgcn_global_load_lds(src, (lds_void*)lds, 16, 0, 0);
+// 16 bytes per lane from one KV page straight into LDS at lds + 16 * lane
+// (buffer_load_dwordx4 ... lds).  The page's base address is wave-uniform
+// (a buffer resource in scalar registers) and each lane adds its byte offset
+// within the page, which the resource bounds to the page.  The buffer form,
+// not global_load_lds: the compiler counts a FLAT-encoded LDS load as a
+// possible out-of-order LDS access too, and then waits for every LDS read in
+// flight (lgkmcnt(0)) wherever one result is needed, which stalls the MFMAs
+// on fragments read ahead of them.  A plain __device__ function: lambdas in
+// kernels are also compiled for the host, where these builtins do not exist.
+__device__ __forceinline__ void load_page_to_lds16(const void* page, uint32_t page_bytes, uint32_t byte_offset,
+                                                   void* lds) {
+  // Raw buffer (stride 0), dword 3 = 0x00020000: 32-bit data format, the
+  // usual CDNA setting for untyped buffer loads.
+  const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(page), (short)0,
+                                                                       (int)page_bytes, 0x00020000);
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_void*)lds, 16, byte_offset, 0, 0, 0);
 }
 
 template <int kNewer>
@@ -238,7 +249,7 @@ __global__ __launch_bounds__(kWaves * 64, 1) void paged_prefill_kernel(PrefillPa
 
   // A stage holds the 64 tokens of one step: tile j0 + 2i (group 0) in rows
   // 0..31 and tile j0 + 2i + 1 (group 1) in rows 32..63.  Tokens move
-  // straight from HBM/L2 into LDS (global_load_lds_dwordx4: lane i of a
+  // straight from HBM/L2 into LDS (buffer_load_dwordx4 ... lds: lane i of a
   // wavefront writes 16 bytes at the wavefront's LDS base + 16 i), so they
   // take no registers and no LDS store instructions.  Wavefront w, step u
   // fills LDS chunks (u*8 + w)*64 .. +63 of a stage; LDS chunk P holds token
@@ -282,10 +293,12 @@ __global__ __launch_bounds__(kWaves * 64, 1) void paged_prefill_kernel(PrefillPa
 #pragma unroll
     for (int u = 0; u < TL::kChunksPerThread; u++) {
       const int tg = min((j0 + 2 * si) * kTileTokens + ld_t[u], s.key_end - 1);
-      const int64_t row = ((pages.pg[u] * p.num_kv_heads + h) * p.page_size + page_mod(tg)) * D;
+      const int64_t page = (pages.pg[u] * p.num_kv_heads + h) * p.page_size * D; // wave-uniform
+      const uint32_t row = (uint32_t)page_mod(tg) * D;
       const int dst = (u * kWaves + wave) * 64 * 8;
-      load_to_lds16(kpool + row + ld_k[u], kb + dst);
-      load_to_lds16(vpool + row + ld_v[u], vb + dst);
+      const uint32_t page_bytes = (uint32_t)p.page_size * D * sizeof(half_t);
+      load_page_to_lds16(kpool + page, page_bytes, (row + ld_k[u]) * (uint32_t)sizeof(half_t), kb + dst);
+      load_page_to_lds16(vpool + page, page_bytes, (row + ld_v[u]) * (uint32_t)sizeof(half_t), vb + dst);
     }
   };
   constexpr int kLoadsPerStage = 2 * TL::kChunksPerThread; // per lane
