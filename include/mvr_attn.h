@@ -190,7 +190,10 @@ size_t mvr_paged_attention_cascade_workspace_size(const mvr_paged_attention_args
 /* mvr_paged_attention with shared prefixes read once per group.  Same
    arguments, output and numerics (an exact split of the softmax sum; results
    differ from the plain call only by rounding).  Stream-ordered, allocates
-   nothing. */
+   nothing.  When the length hints show that the shared reads are a small
+   part of the call's key reads (below MVR_ATTN_CASCADE_MIN_SAVING percent,
+   default 25), the call runs as mvr_paged_attention instead, which is then
+   faster; the workspace size above follows the same choice. */
 int mvr_paged_attention_cascade(const mvr_paged_attention_args* args, const mvr_cascade_groups* groups);
 
 /* Host-side checks of the group tables: members consecutive and aligned with

@@ -542,19 +542,23 @@ def make_cascade_groups(group_cu_q_lens, group_prefix_lens, group_block_tables, 
 
 def paged_attention_cascade(q, key_pool, value_pool, block_tables, seq_lens, cu_q_lens, groups: CascadeGroups,
                             out=None, *, max_q_len: int, max_seq_len: int, scale: float = 0.0, workspace=None,
-                            stream=None, sum_seq_lens: int = 0):
-    """paged_attention with each group's shared prefix attended once; returns out [Hq, total_q, D]."""
+                            stream=None, sum_seq_lens: int = 0, seq_lens_host=None, cu_q_lens_host=None):
+    """paged_attention with each group's shared prefix attended once; returns out [Hq, total_q, D].  (With the
+    sum_prefix_lens hint showing little sharing, the library runs the plain call instead.)"""
     torch = _torch()
     with _stream_scope(stream, q, key_pool, value_pool, block_tables, seq_lens, cu_q_lens, out, workspace,
                        *groups._keep):
         if out is None:
             out = torch.empty_like(q, memory_format=torch.contiguous_format)
         a = make_args(q, key_pool, value_pool, block_tables, seq_lens, cu_q_lens, out, max_q_len=max_q_len,
-                      max_seq_len=max_seq_len, scale=scale, stream=stream, sum_seq_lens=sum_seq_lens)
+                      max_seq_len=max_seq_len, scale=scale, stream=stream, sum_seq_lens=sum_seq_lens,
+                      seq_lens_host=seq_lens_host, cu_q_lens_host=cu_q_lens_host)
         lib = load_library()
         need = int(lib.mvr_paged_attention_cascade_workspace_size(ctypes.byref(a), ctypes.byref(groups)))
         if need == 0:
-            _check(lib.mvr_paged_attention_cascade(ctypes.byref(a), ctypes.byref(groups)))  # raises with the reason
+            # An invalid call raises with the reason; a valid one (the plain path, at times) needs no workspace.
+            _check(lib.mvr_paged_attention_cascade(ctypes.byref(a), ctypes.byref(groups)))
+            return out
         if workspace is None or workspace.numel() * workspace.element_size() < need:
             workspace = new_workspace(need, q.device)
         a.workspace = workspace.data_ptr()

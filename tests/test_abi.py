@@ -326,6 +326,26 @@ def test_cascade_scalar_checks_reject_before_launch():
     assert lib.mvr_paged_attention_cascade_workspace_size(ctypes.byref(a), ctypes.byref(_groups())) > 0
 
 
+def test_cascade_falls_back_to_the_plain_call_when_sharing_is_small():
+    lib = M.load_library()
+    size = lambda a, g: lib.mvr_paged_attention_cascade_workspace_size(ctypes.byref(a), ctypes.byref(g))
+    # 16 sequences of 5 query tokens, 139264 cached tokens in all; 4 groups share 1024 tokens each: 12288 reads
+    # saved (9%), so the call runs as mvr_paged_attention and needs its workspace
+    a = _args(num_seqs=16, max_q_len=5, max_seq_len=16384, max_pages_per_seq=1024, num_pages=32768,
+              sum_seq_lens=139264)
+    small = _groups(num_groups=4, max_group_q_len=20, max_prefix_len=1024, sum_prefix_lens=16 * 1024)
+    assert size(a, small) == lib.mvr_paged_attention_workspace_size(ctypes.byref(a))
+    state = a.num_q_heads * a.num_seqs * a.max_q_len * a.head_dim * 4  # the cascade's per-row prefix state
+    small.sum_prefix_lens = 0  # without the hint the cascade runs as asked
+    assert size(a, small) >= state
+    # 64 decode sequences behind one 8192-token prompt: 63 * 8192 of 64 * 9344 reads saved (86%)
+    b = _args(num_seqs=64, max_q_len=1, max_seq_len=10240, max_pages_per_seq=640, num_pages=40000,
+              sum_seq_lens=64 * 9344)
+    big = _groups(num_groups=1, max_group_q_len=64, max_prefix_len=8192, sum_prefix_lens=64 * 8192)
+    assert size(b, big) >= b.num_q_heads * b.num_seqs * b.head_dim * 4
+    assert size(b, big) != lib.mvr_paged_attention_workspace_size(ctypes.byref(b))
+
+
 def test_cascade_validate_checks_the_groups():
     # two sequences of one token each, 16-token pages; both share the first 32 tokens (2 pages)
     a = _args(max_q_len=1, max_seq_len=1024)

@@ -8,7 +8,9 @@ of the groups.  Covers the speculative-verification workload's own groups (4 x
 4 sequences sharing 1024 tokens), ragged groups with a lone sequence and a
 group of one, a prefix pass that takes the chunked-prefill kernel (many rows
 per group), F32 and head_dim 64, a call with no group at all, and a decode
-batch of 64 sequences sharing one 8192-token prompt (plain call checked too).
+batch of 64 sequences sharing one 8192-token prompt (plain call checked too).  With the sum_prefix_lens
+hint, the verification workload (shared reads 9% of the key reads) runs as the plain call, bit for bit, and
+the shared prompt (86%) still cascades.
 """
 import math
 import sys
@@ -44,8 +46,10 @@ def dev(a):
     return torch.from_numpy(np.ascontiguousarray(a)).cuda()
 
 
-def run_cascade(w, t, groups, prefix_of_seq):
-    """groups: consecutive (first_seq, n_seqs, prefix_len) from sequence 0 on; prefix 0 = a member shares nothing."""
+def run_cascade(w, t, groups, prefix_of_seq, hint=False):
+    """groups: consecutive (first_seq, n_seqs, prefix_len) from sequence 0 on; prefix 0 = a member shares nothing.
+    Without the sum_prefix_lens hint (the default here) the library always takes the cascade path; with it, a call
+    whose shared reads are a small part of its key reads runs as the plain call."""
     cu = w.cu_q_lens
     gcu = np.array([cu[g[0]] for g in groups] + ([cu[groups[-1][0] + groups[-1][1]]] if groups else [0]), np.int32)
     gpre = np.array([g[2] for g in groups], np.int32)
@@ -55,7 +59,7 @@ def run_cascade(w, t, groups, prefix_of_seq):
     max_pre = max((g[2] for g in groups), default=1)
     G = M.make_cascade_groups(dev(gcu) if groups else None, dev(gpre) if groups else None,
                               dev(gbt) if groups else None, dev(spre), max_group_q_len=max_gq,
-                              max_prefix_len=max_pre, sum_prefix_lens=int(spre.sum()))
+                              max_prefix_len=max_pre, sum_prefix_lens=int(spre.sum()) if hint else 0)
     args = M.make_args(t["q"], t["key_pool"], t["value_pool"], t["block_tables"], t["seq_lens"], t["cu_q_lens"],
                        t["q"], max_q_len=w.max_q_len, max_seq_len=w.max_seq_len)
     M.validate_cascade(args, G, w.block_tables, w.seq_lens, cu, gcu if groups else None, gpre if groups else None,
@@ -160,3 +164,26 @@ def test_no_groups_equals_plain_call():
     t = W.device_tensors(w, vals)
     got = run_cascade(w, t, [], [0] * w.num_seqs)
     check(w, vals, got, "no groups")
+
+
+def test_small_sharing_runs_as_the_plain_call():
+    # The verification workload's 4 groups share 1024 tokens each: 12288 of ~139K key reads saved, below the 25%
+    # that the cascade needs to pay, so with the hint the call is the plain call (the same launches, same bits).
+    w = W.llama3_8b_spec_verify_f16()
+    vals = W.host_values(w)
+    t = W.device_tensors(w, vals)
+    got = run_cascade(w, t, [(4 * g, 4, 1024) for g in range(4)], [1024] * 16, hint=True)
+    plain = M.paged_attention(t["q"], t["key_pool"], t["value_pool"], t["block_tables"], t["seq_lens"],
+                              t["cu_q_lens"], max_q_len=w.max_q_len, max_seq_len=w.max_seq_len,
+                              sum_seq_lens=int(w.seq_lens.sum()))
+    torch.cuda.synchronize()
+    assert np.array_equal(got, plain.float().cpu().numpy())
+    check(w, vals, got, "spec-verify with the sharing hint (plain path)")
+
+
+def test_large_sharing_still_cascades():
+    w = W.llama3_8b_shared_prompt_decode_f16()
+    vals = W.host_values(w)
+    t = W.device_tensors(w, vals)
+    got = run_cascade(w, t, [(0, w.num_seqs, 8192)], [8192] * w.num_seqs, hint=True)
+    check(w, vals, got, "shared prompt with the sharing hint (cascade path)")
