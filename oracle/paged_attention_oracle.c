@@ -150,6 +150,19 @@ static size_t pool_index(const group_ctx* c, int64_t page, int h, int t, int d) 
   return (((size_t)page * c->Hkv + h) * c->P + t) * c->D + d;
 }
 
+/* The reference's checks on the page list (common.rs:758-781): every page
+   that holds keys lies inside the pool, and the pages cover the length. */
+static int check_page_list(const group_ctx* c) {
+  int remaining = c->cached_token_count;
+  for (int64_t pi = 0; pi < c->num_page_ids; pi++) {
+    const int slice = remaining < c->P ? remaining : c->P;
+    const int64_t page = c->page_ids[pi];
+    if (slice > 0 && (page < 0 || page >= c->page_count)) return ORACLE_E_PAGE_ID;
+    remaining -= slice;
+  }
+  return remaining == 0 ? 0 : ORACLE_E_UNCOVERED;
+}
+
 /* Returns 0 or ORACLE_E_*; writes one group's output rows. */
 static int attend_group(const group_ctx* c, int kv_head, int mode, double* y /* [rep*q][D] */,
                         float* scratch /* [rep*q][L] */, float* vcat /* [L][D] */) {
@@ -159,7 +172,10 @@ static int attend_group(const group_ctx* c, int kv_head, int mode, double* y /* 
   const int dtype = c->dtype;
 
   if (mode == ORACLE_EXACT_F64) {
-    /* Independent double-precision attention: no per-op rounding. */
+    /* Independent double-precision attention: no per-op rounding.  It reads
+       the pool through the same page list, so the same checks come first. */
+    const int pc = check_page_list(c);
+    if (pc != 0) return pc;
     double* s = (double*)malloc(sizeof(double) * (size_t)(L > 0 ? L : 1));
     if (!s) return ORACLE_E_ALLOC;
     const double scale = 1.0 / sqrt((double)D);
