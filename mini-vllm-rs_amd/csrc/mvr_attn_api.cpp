@@ -248,13 +248,27 @@ mvr::PagedAttentionPlan make_plan(const mvr_paged_attention_args* a, bool allow_
   if (cpp > max_chunks) cpp = max_chunks;
   plan.chunks_per_part = cpp;
   plan.max_parts = (max_chunks + cpp - 1) / cpp;
-  // Block merge: a uniform batch split into exactly one block's worth of
-  // partitions (the batch-64 x 8K decode: 4 x 2048 tokens) puts the
-  // partitions of one (sequence, KV head, row tile) in one block and merges
-  // them in LDS, without partials in HBM or a merge launch; its blocks need
-  // no XCD padding.  MVR_ATTN_BLOCK_MERGE=false keeps the separate merge.
+  // Block merge: a uniform batch split into at most one block's worth of
+  // partitions (the batch-64 x 8K decode: 4 x 2048 tokens; one 512-token
+  // sequence: 16 x 32 tokens) puts the partitions of one (sequence, KV head,
+  // row tile) in one block of 4, 8 or 16 wavefronts and merges them in LDS,
+  // without partials in HBM or a merge launch (about 8 us of launch gap and
+  // kernel time).  Wavefronts past a tile's partitions idle through the
+  // block's barriers, so a block is used only when at least three quarters of
+  // its wavefronts hold a partition.  The wider blocks put a whole tile on
+  // one CU, which suits F16 only: F32 products (v_mfma_f32_16x16x4_f32) made
+  // one 512-token F32 sequence MFMA-bound on its CU, 14.8 us in 16-wavefront
+  // blocks against 7.2 + 4.7 us for the same partitions spread over 8 CUs and
+  // merged by a second launch.  Blocks of 16 wavefronts (128 VGPRs per lane)
+  // for head_dim 64 only.  MVR_ATTN_BLOCK_MERGE=false keeps the separate merge.
   static const bool block_merge_enabled = env_bool("MVR_ATTN_BLOCK_MERGE", true);
-  plan.block_merge = block_merge_enabled && !ragged && plan.row_blocks == 1 && plan.max_parts == mvr::kWavesPerBlock;
+  plan.block_waves = 0;
+  if (block_merge_enabled && !ragged && plan.row_blocks == 1) {
+    const int widest = a->dtype != MVR_DTYPE_F16 ? 4 : a->head_dim == 64 ? 16 : 8;
+    for (int w = 4; w <= widest && plan.block_waves == 0; w *= 2)
+      if (plan.max_parts <= w && 4 * plan.max_parts >= 3 * w) plan.block_waves = w;
+  }
+  plan.block_merge = plan.block_waves > 0;
   // Dense layout for ragged batches with one row tile (dense_unit in
   // paged_attention.hip): the live units are numbered from 0, so in-order
   // dispatch balances them over the CUs and XCDs, where slot == partition
@@ -317,7 +331,7 @@ mvr::PagedAttentionPlan make_plan(const mvr_paged_attention_args* a, bool allow_
   // 3,925 GB/s against 5,683 unpadded, and 48, 96 and 128 sequences gained
   // 34-52% at 512..8K tokens.  Unpadded was equal or better on every other
   // workload measured, the verify workload with its shared prefixes included.
-  plan.num_units = base_units * plan.max_parts;
+  plan.num_units = base_units * (plan.block_merge ? plan.block_waves : plan.max_parts);
   plan.partial_bytes = 0;
   if (plan.max_parts > 1 && !plan.block_merge) {
     // [partial o][partial m, l]

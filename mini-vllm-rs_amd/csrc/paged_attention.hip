@@ -356,13 +356,14 @@ struct F32Traits {
 // Occupancy floor (blocks per CU = wavefronts per SIMD) per dtype: the
 // largest that fits each variant without scratch.
 //
-// BM (block merge): a block holds the kWavesPerBlock partitions of one
+// BM (block merge): a block of WPB wavefronts holds the partitions of one
 // (sequence, KV head, row tile) instead of one partition of kWavesPerBlock
 // KV heads, and merges them through LDS at the end: no fp32 partials in HBM
-// and no merge launch.  The planner uses it when a uniform batch splits
-// every context into exactly kWavesPerBlock partitions (the wavefronts of a
-// block then do equal work); a partition without keys still takes part in
-// the block's barrier.
+// and no merge launch (which costs about 8 us of launch gap and kernel time
+// whatever its work).  The planner uses it when a uniform batch splits every
+// context into more than WPB / 2 and at most WPB partitions, WPB = 4, 8 or
+// 16 (the wavefronts of a block then do near-equal work); a partition
+// without keys still takes part in the block's barriers.
 // DENSE: the dense layout of a ragged batch (dense_unit); a separate instantiation,
 // so that the slot == partition kernels compile exactly as without it.
 // DEPTH: chunks in flight per wavefront.  3 (deep_pipeline plans: 16-row
@@ -371,24 +372,35 @@ struct F32Traits {
 // sequences, whose live wavefronts do not fill the device and wait on
 // latency (16 sequences of 1.9K..14.8K tokens: 120 -> 106 us), and loses
 // where a third wavefront per SIMD had work (128 ragged sequences).
-template <typename Tr, int D, int NB, bool BM = false, bool DENSE = false, int DEPTH = 2>
-__global__ __launch_bounds__(kWaveSize* kWavesPerBlock, DEPTH == 3 ? 2 : Tr::template min_blocks<NB>()) void
+// Block shape of a variant: WPB wavefronts; 16-wavefront blocks (4 per SIMD)
+// leave 128 VGPRs per lane.
+template <typename Tr, int NB, int DEPTH, int WPB>
+constexpr int kernel_min_blocks() {
+  return WPB > kWavesPerBlock ? 1 : (DEPTH == 3 ? 2 : Tr::template min_blocks<NB>());
+}
+
+template <typename Tr, int D, int NB, bool BM = false, bool DENSE = false, int DEPTH = 2, int WPB = kWavesPerBlock>
+__global__ __launch_bounds__(kWaveSize* WPB, (kernel_min_blocks<Tr, NB, DEPTH, WPB>())) void
     paged_attention_kernel(PagedAttentionParams p) {
   typedef typename Tr::elem T;
   constexpr int kTileRows = 16 * NB;
   static_assert(DEPTH == 2 || (DEPTH == 3 && NB == 1 && D * sizeof(T) <= 256 && !BM), "unsupported pipeline depth");
-  __shared__ __attribute__((aligned(16))) T lds_all[kWavesPerBlock][kChunkTokens * D];
-  // BM: each wavefront's rows (O, m, l); rows padded by 4 floats so that the
-  // 16 rows of a float4 store fall in distinct banks.
+  static_assert(BM || WPB == kWavesPerBlock, "only block-merge plans change the block shape");
+  // Each wavefront's V tile, and (BM, after the key loop) each wavefront's
+  // rows (O, m, l) in the same LDS: rows padded by 4 floats so that the 16
+  // rows of a float4 store fall in distinct banks.
   constexpr int kMergeStride = D + 4;
-  __shared__ __attribute__((aligned(16))) float merge_o[BM ? kWavesPerBlock * kTileRows * kMergeStride : 4];
-  __shared__ float merge_ml[BM ? kWavesPerBlock * kTileRows * 2 : 2];
+  constexpr size_t kTileBytes = (size_t)WPB * kChunkTokens * D * sizeof(T);
+  constexpr size_t kMergeBytes = BM ? (size_t)WPB * kTileRows * (kMergeStride + 2) * sizeof(float) : 0;
+  __shared__ __attribute__((aligned(16))) char lds_raw[kTileBytes > kMergeBytes ? kTileBytes : kMergeBytes];
+  float* const merge_o = reinterpret_cast<float*>(lds_raw);
+  float* const merge_ml = merge_o + WPB * kTileRows * kMergeStride;
 
   const int l = lane_id();
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWaveSize);
-  const int64_t unit = (int64_t)blockIdx.x * kWavesPerBlock + wave;
+  const int64_t unit = (int64_t)blockIdx.x * WPB + wave;
   if (!BM && unit >= p.num_units) return; // BM grids are exact: no wavefront may skip the block barrier
-  T* lds = lds_all[wave];
+  T* lds = reinterpret_cast<T*>(lds_raw) + (size_t)wave * kChunkTokens * D;
 
   // KV head fastest: the wavefronts of one (sequence, partition) read the
   // adjacent per-head slabs of the same pages at about the same time, and
@@ -549,8 +561,10 @@ __global__ __launch_bounds__(kWaveSize* kWavesPerBlock, DEPTH == 3 ? 2 : Tr::tem
   if constexpr (BM) {
     // Every wavefront's rows into LDS (a partition without keys holds
     // m = -inf, l = 0, O = 0 and lies past n_parts), then each wavefront
-    // merges rows wave, wave + 4, ... with the arithmetic of
-    // merge_partitions_kernel (same order, so the same bits).
+    // merges rows wave, wave + WPB, ... with the arithmetic of
+    // merge_partitions_kernel (same order, so the same bits).  The rows
+    // overlay the V tiles: every wavefront leaves its key loop first.
+    __syncthreads();
 #pragma unroll
     for (int nb = 0; nb < NB; nb++) {
       const float ltot = wave_sum_across_groups(lsum[nb]);
@@ -564,31 +578,41 @@ __global__ __launch_bounds__(kWaveSize* kWavesPerBlock, DEPTH == 3 ? 2 : Tr::tem
       }
     }
     __syncthreads();
-    static_assert(kWavesPerBlock == 4, "the den sum below follows a 4-partition butterfly");
+    static_assert(WPB == 4 || WPB == 8 || WPB == 16, "the den sum below is a butterfly over WPB lanes");
     constexpr int kPer = D / kWaveSize;
     // At most one partition per wavefront holds a result (seq_len is clamped to
-    // max_seq_len, which the plan splits into exactly kWavesPerBlock parts).
-    const int n_held = min(n_parts, kWavesPerBlock);
-    for (int rr = wave; rr < kTileRows; rr += kWavesPerBlock) {
+    // max_seq_len, which the plan splits into at most WPB parts).
+    const int n_held = min(n_parts, WPB);
+    for (int rr = wave; rr < kTileRows; rr += WPB) {
       const int rho = rt * kTileRows + rr;
       if (rho >= rows || n_held == 0) continue;
-      float mj[kWavesPerBlock], wl[kWavesPerBlock];
+      float mj[WPB], wl[WPB];
       float mmax = -INFINITY;
 #pragma unroll
-      for (int j = 0; j < kWavesPerBlock; j++) {
+      for (int j = 0; j < WPB; j++) {
         mj[j] = j < n_held ? merge_ml[(j * kTileRows + rr) * 2] : -INFINITY;
         mmax = fmaxf(mmax, mj[j]);
       }
       const float m_use = mmax == -INFINITY ? 0.f : mmax;
-      float w[kWavesPerBlock];
+      float w[WPB];
 #pragma unroll
-      for (int j = 0; j < kWavesPerBlock; j++) {
+      for (int j = 0; j < WPB; j++) {
         w[j] = j < n_held ? __builtin_amdgcn_exp2f(mj[j] - m_use) : 0.f;
         wl[j] = j < n_held ? w[j] * merge_ml[(j * kTileRows + rr) * 2 + 1] : 0.f;
       }
       // merge_partitions_kernel sums lane j's w_j l_j over the wavefront by
-      // xor-shuffles; with partitions in lanes 0..3 that is (0 + 2) + (1 + 3).
-      const float den = (wl[0] + wl[2]) + (wl[1] + wl[3]);
+      // xor-shuffles at offsets 32, 16, ..., 1; with the partitions in lanes
+      // 0..WPB-1 (0 elsewhere) the steps above WPB / 2 add zeros, and the
+      // rest is this butterfly (lane 0's value).
+#pragma unroll
+      for (int off = WPB / 2; off >= 1; off >>= 1) {
+        float t[WPB];
+#pragma unroll
+        for (int j = 0; j < WPB; j++) t[j] = wl[j] + wl[j ^ off];
+#pragma unroll
+        for (int j = 0; j < WPB; j++) wl[j] = t[j];
+      }
+      const float den = wl[0];
       float acc[kPer];
 #pragma unroll
       for (int e = 0; e < kPer; e++) acc[e] = 0.f;
@@ -681,7 +705,6 @@ __global__ __launch_bounds__(256) void merge_partitions_kernel(PagedAttentionPar
   constexpr int kTileRows = 16 * NB;
   constexpr int kBlocksPerTile = kTileRows / kWavesPerBlock;
   constexpr int kPer = D / kWaveSize; // output elements per lane
-  constexpr int kInFlight = 8;
   const int tile = blockIdx.x / kBlocksPerTile;
   const int lr = (blockIdx.x % kBlocksPerTile) * kWavesPerBlock + __builtin_amdgcn_readfirstlane(threadIdx.x / kWaveSize);
   const int l = lane_id();
@@ -698,6 +721,20 @@ __global__ __launch_bounds__(256) void merge_partitions_kernel(PagedAttentionPar
 
   // Partial row of partition j: (tile * max_parts + j) * kTileRows + lr.
   const int64_t prow0 = (int64_t)tile * p.max_parts * kTileRows + lr;
+  // Up to 64 partial rows (one round) are loaded at once, and the first
+  // round's loads are issued beside the (m, l) loads: one round trip to
+  // memory instead of one per few rows (64 partials of a small decode took
+  // 8 dependent round trips when streamed 8 rows at a time).
+  float v[kWaveSize][kPer];
+  auto load_round = [&](int j0, int cnt) __attribute__((always_inline)) {
+    const float* base = p.partial_o + (prow0 + (int64_t)j0 * kTileRows) * D + l * kPer;
+#pragma unroll
+    for (int u = 0; u < kWaveSize; u++)
+      if (u < cnt)
+#pragma unroll
+        for (int e = 0; e < kPer; e++) v[u][e] = base[(int64_t)u * kTileRows * D + e];
+  };
+  load_round(0, min(kWaveSize, n_parts));
   float mmax = -INFINITY;
   for (int j = l; j < n_parts; j += kWaveSize) mmax = fmaxf(mmax, p.partial_ml[(prow0 + (int64_t)j * kTileRows) * 2]);
 #pragma unroll
@@ -716,26 +753,15 @@ __global__ __launch_bounds__(256) void merge_partitions_kernel(PagedAttentionPar
       den += w * p.partial_ml[prow * 2 + 1];
     }
     const int cnt = min(kWaveSize, n_parts - j0);
-    const float* base = p.partial_o + (prow0 + (int64_t)j0 * kTileRows) * D + l * kPer;
-    int jj = 0;
-    for (; jj + kInFlight <= cnt; jj += kInFlight) {
-      float v[kInFlight][kPer];
+    if (j0 > 0) load_round(j0, cnt);
+    // o = sum_j w_j o_j, in partition order.
 #pragma unroll
-      for (int u = 0; u < kInFlight; u++)
-#pragma unroll
-        for (int e = 0; e < kPer; e++) v[u][e] = base[(int64_t)(jj + u) * kTileRows * D + e];
-#pragma unroll
-      for (int u = 0; u < kInFlight; u++) {
-        const float wu = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), jj + u));
+    for (int u = 0; u < kWaveSize; u++)
+      if (u < cnt) {
+        const float wu = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), u));
 #pragma unroll
         for (int e = 0; e < kPer; e++) acc[e] = fmaf(wu, v[u][e], acc[e]);
       }
-    }
-    for (; jj < cnt; jj++) {
-      const float wu = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), jj));
-#pragma unroll
-      for (int e = 0; e < kPer; e++) acc[e] = fmaf(wu, base[(int64_t)jj * kTileRows * D + e], acc[e]);
-    }
   }
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) den += __shfl_xor(den, off);
@@ -767,12 +793,26 @@ hipError_t launch_typed(const PagedAttentionPlan& plan, const PagedAttentionPara
   const int64_t blocks = (plan.num_units + kWavesPerBlock - 1) / kWavesPerBlock;
   if constexpr (NB == 1) {
     if (plan.block_merge) {
-      // One block per (sequence, KV head, row tile): exactly num_units / 4 blocks.
-      if (plan.max_parts != kWavesPerBlock ||
-          plan.num_units != (int64_t)params.num_seqs * params.num_kv_heads * params.row_tiles * kWavesPerBlock)
+      // One block of block_waves wavefronts per (sequence, KV head, row tile).
+      const int64_t tiles = (int64_t)params.num_seqs * params.num_kv_heads * params.row_tiles;
+      if (plan.max_parts > plan.block_waves || plan.num_units != tiles * plan.block_waves) return hipErrorInvalidValue;
+      if (plan.block_waves == 4) {
+        hipLaunchKernelGGL((paged_attention_kernel<Tr, D, NB, true, false, 2, 4>), dim3((unsigned)tiles),
+                           dim3(kWaveSize * 4), 0, stream, params);
+      } else if (plan.block_waves == 8) {
+        hipLaunchKernelGGL((paged_attention_kernel<Tr, D, NB, true, false, 2, 8>), dim3((unsigned)tiles),
+                           dim3(kWaveSize * 8), 0, stream, params);
+      } else if (plan.block_waves == 16) {
+        // 16 wavefronts per block leave 128 VGPRs per lane: head_dim 64 only.
+        if constexpr (D == 64) {
+          hipLaunchKernelGGL((paged_attention_kernel<Tr, D, NB, true, false, 2, 16>), dim3((unsigned)tiles),
+                             dim3(kWaveSize * 16), 0, stream, params);
+        } else {
+          return hipErrorInvalidValue;
+        }
+      } else {
         return hipErrorInvalidValue;
-      hipLaunchKernelGGL((paged_attention_kernel<Tr, D, NB, true>), dim3((unsigned)blocks),
-                         dim3(kWaveSize * kWavesPerBlock), 0, stream, params);
+      }
       return hipGetLastError();
     }
   }

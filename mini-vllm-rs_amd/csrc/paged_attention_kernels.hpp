@@ -68,7 +68,8 @@ struct PagedAttentionPlan {
   size_t partial_bytes; // workspace for partials (0 when max_parts == 1)
   bool prefill;         // chunked-prefill kernel (paged_prefill.hip) instead of the split-context one
   int kv_splits;        // prefill: key-range splits per 128-row tile
-  bool block_merge;     // max_parts == kWavesPerBlock: one block per tile, partitions merged in LDS
+  bool block_merge;     // one block per tile, its partitions merged in LDS
+  int block_waves;      // block_merge: wavefronts per block, 4, 8 or 16 (>= max_parts)
   bool dense_parts;     // ragged split plan: live units first, in a dense order (see dense_unit)
   bool deep_pipeline;   // three chunks in flight per wavefront instead of two (16-row tiles only)
 };

@@ -243,23 +243,25 @@ def test_workspace_reuse_across_shapes():
         assert torch.equal(again, first[idx])
 
 
-def test_many_small_partitions_and_many_tiles():
+@pytest.mark.parametrize("block_merge", ["false", "true"])
+def test_many_small_partitions_and_many_tiles(block_merge):
     """16800 (sequence, kv head) tiles, each split into 5-7 partitions of 2 chunks (forced with
-    MVR_ATTN_CHUNKS_PER_PARTITION=2, read once per process, hence the child process): the merge of many partials
-    per tile still matches the oracle."""
+    MVR_ATTN_CHUNKS_PER_PARTITION=2, read once per process, hence the child process), planned as uniform: with
+    MVR_ATTN_BLOCK_MERGE=false the merge kernel combines many partials per tile, by default each tile is one block of
+    8 wavefronts merging in LDS; both match the oracle."""
     import subprocess
 
     root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
     path = os.pathsep.join([os.path.join(root, "mini-vllm-rs_amd"), os.path.join(root, "oracle"),
                             os.environ.get("PYTHONPATH", "")])
-    env = dict(os.environ, MVR_ATTN_CHUNKS_PER_PARTITION="2", PYTHONPATH=path)
-    r = subprocess.run([sys.executable, "-u", __file__, "many-partitions-child"], env=env, capture_output=True,
-                       text=True, timeout=300)
+    env = dict(os.environ, MVR_ATTN_CHUNKS_PER_PARTITION="2", MVR_ATTN_BLOCK_MERGE=block_merge, PYTHONPATH=path)
+    r = subprocess.run([sys.executable, "-u", __file__, "many-partitions-child", block_merge], env=env,
+                       capture_output=True, text=True, timeout=300)
     say(r.stdout[-2000:] + r.stderr[-2000:])
     assert r.returncode == 0
 
 
-def _many_partitions_child():
+def _many_partitions_child(block_merge):
     rng = np.random.default_rng(33)
     B, hq, hkv, D, P = 2100, 8, 8, 64, 16
     seq_lens = rng.integers(130, 200, size=B).astype(np.int32)
@@ -276,8 +278,10 @@ def _many_partitions_child():
     t = W.device_tensors(w, vals)
     a = M.make_args(t["q"], t["key_pool"], t["value_pool"], t["block_tables"], t["seq_lens"], t["cu_q_lens"],
                     torch.empty_like(t["q"]), max_q_len=1, max_seq_len=w.max_seq_len)
-    assert M.workspace_size(a) > 0
-    out = run_hip(w, t).float().cpu().numpy()
+    # planned as uniform (no length hint): the two-launch plan keeps fp32 partials in the workspace, the block-merge
+    # plan needs none; the two-launch run keeps the length hint (the ragged plan), the block-merge run omits it
+    assert (M.workspace_size(a) == 0) == (block_merge == "true")
+    out = run_hip(w, t, hint=block_merge == "false").float().cpu().numpy()
     ref = run_oracle(w, vals)
     err = np.abs(out - ref).max()
     print(f"many partitions: {B} sequences x {hkv} kv heads, max-abs vs oracle {err:.3e}", flush=True)
@@ -384,8 +388,8 @@ def test_poisoned_tail_slots_and_foreign_pages_are_ignored():
     assert torch.equal(a, b)
 
 
-if __name__ == "__main__" and len(sys.argv) > 1 and sys.argv[1] == "many-partitions-child":
-    _many_partitions_child()
+if __name__ == "__main__" and len(sys.argv) > 2 and sys.argv[1] == "many-partitions-child":
+    _many_partitions_child(sys.argv[2])
 
 
 def _same_tokens_two_page_sizes(seed, dtype, hq, hkv, d, seq_lens, q_lens, page_size):
