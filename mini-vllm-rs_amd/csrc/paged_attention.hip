@@ -705,6 +705,7 @@ __global__ __launch_bounds__(256) void merge_partitions_kernel(PagedAttentionPar
   constexpr int kTileRows = 16 * NB;
   constexpr int kBlocksPerTile = kTileRows / kWavesPerBlock;
   constexpr int kPer = D / kWaveSize; // output elements per lane
+  constexpr int kInFlight = 8;
   const int tile = blockIdx.x / kBlocksPerTile;
   const int lr = (blockIdx.x % kBlocksPerTile) * kWavesPerBlock + __builtin_amdgcn_readfirstlane(threadIdx.x / kWaveSize);
   const int l = lane_id();
@@ -721,20 +722,6 @@ __global__ __launch_bounds__(256) void merge_partitions_kernel(PagedAttentionPar
 
   // Partial row of partition j: (tile * max_parts + j) * kTileRows + lr.
   const int64_t prow0 = (int64_t)tile * p.max_parts * kTileRows + lr;
-  // Up to 64 partial rows (one round) are loaded at once, and the first
-  // round's loads are issued beside the (m, l) loads: one round trip to
-  // memory instead of one per few rows (64 partials of a small decode took
-  // 8 dependent round trips when streamed 8 rows at a time).
-  float v[kWaveSize][kPer];
-  auto load_round = [&](int j0, int cnt) __attribute__((always_inline)) {
-    const float* base = p.partial_o + (prow0 + (int64_t)j0 * kTileRows) * D + l * kPer;
-#pragma unroll
-    for (int u = 0; u < kWaveSize; u++)
-      if (u < cnt)
-#pragma unroll
-        for (int e = 0; e < kPer; e++) v[u][e] = base[(int64_t)u * kTileRows * D + e];
-  };
-  load_round(0, min(kWaveSize, n_parts));
   float mmax = -INFINITY;
   for (int j = l; j < n_parts; j += kWaveSize) mmax = fmaxf(mmax, p.partial_ml[(prow0 + (int64_t)j * kTileRows) * 2]);
 #pragma unroll
@@ -753,15 +740,26 @@ __global__ __launch_bounds__(256) void merge_partitions_kernel(PagedAttentionPar
       den += w * p.partial_ml[prow * 2 + 1];
     }
     const int cnt = min(kWaveSize, n_parts - j0);
-    if (j0 > 0) load_round(j0, cnt);
-    // o = sum_j w_j o_j, in partition order.
+    const float* base = p.partial_o + (prow0 + (int64_t)j0 * kTileRows) * D + l * kPer;
+    int jj = 0;
+    for (; jj + kInFlight <= cnt; jj += kInFlight) {
+      float v[kInFlight][kPer];
 #pragma unroll
-    for (int u = 0; u < kWaveSize; u++)
-      if (u < cnt) {
-        const float wu = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), u));
+      for (int u = 0; u < kInFlight; u++)
+#pragma unroll
+        for (int e = 0; e < kPer; e++) v[u][e] = base[(int64_t)(jj + u) * kTileRows * D + e];
+#pragma unroll
+      for (int u = 0; u < kInFlight; u++) {
+        const float wu = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), jj + u));
 #pragma unroll
         for (int e = 0; e < kPer; e++) acc[e] = fmaf(wu, v[u][e], acc[e]);
       }
+    }
+    for (; jj < cnt; jj++) {
+      const float wu = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), jj));
+#pragma unroll
+      for (int e = 0; e < kPer; e++) acc[e] = fmaf(wu, base[(int64_t)jj * kTileRows * D + e], acc[e]);
+    }
   }
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) den += __shfl_xor(den, off);
