@@ -305,6 +305,7 @@ def main():
     ap.add_argument("--only-config", type=int, default=0, choices=(0, 1, 2, 4, 5),
                     help="time only this one of the other workloads and print its result (for profiling one kernel)")
     ap.add_argument("--only-mixed", action="store_true", help="time only the mixed decode + prefill batch")
+    ap.add_argument("--f32", action="store_true", help="with --only-config 4: the same chunked prefill in F32")
     a = ap.parse_args()
     if a.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {a.gpus} is not supported: the attention path runs on one "
@@ -324,9 +325,13 @@ def main():
     if a.only_mixed:
         print(json.dumps({"mixed": measure_mixed(W, M, torch, a.steps, a.warmup)}), flush=True)
         return
+    if a.f32 and a.only_config != 4:
+        print("--f32 goes with --only-config 4", file=sys.stderr)
+        sys.exit(2)
     if a.only_config:
-        log(f"[bench] config {a.only_config} only")
-        res = measure(W, M, torch, a.only_config, a.steps, a.warmup)
+        log(f"[bench] config {a.only_config} only{' (F32)' if a.f32 else ''}")
+        cfg = (lambda: W.qwen2_7b_chunked_prefill_f16("f32")) if a.f32 else a.only_config
+        res = measure(W, M, torch, cfg, a.steps, a.warmup)
         print(json.dumps({"config": a.only_config, "steps": a.steps, "warmup": a.warmup, **res}), flush=True)
         return
     headline_cfg = 3

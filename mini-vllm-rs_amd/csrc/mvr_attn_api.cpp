@@ -171,11 +171,11 @@ mvr::PagedAttentionPlan make_plan(const mvr_paged_attention_args* a, bool allow_
   const int group = a->num_q_heads / a->num_kv_heads;
   const int64_t rows_max = (int64_t)group * a->max_q_len;
   // Many query rows per KV head (chunked prefill): dense contraction, use the
-  // LDS-shared 32x32 MFMA kernel.  MVR_ATTN_PREFILL_KERNEL=false keeps every
-  // call on the split-context kernel.
+  // LDS-shared 32x32 MFMA kernel (F16 32x32x16, F32 32x32x2).
+  // MVR_ATTN_PREFILL_KERNEL=false keeps every call on the split-context kernel.
   static const bool prefill_enabled = env_bool("MVR_ATTN_PREFILL_KERNEL", true);
   const bool page_pow2 = (a->page_size & (a->page_size - 1)) == 0;
-  if (allow_prefill && prefill_enabled && a->dtype == MVR_DTYPE_F16 && rows_max > 64 && page_pow2) {
+  if (allow_prefill && prefill_enabled && rows_max > 64 && page_pow2) {
     plan.prefill = true;
     plan.row_tiles = (int)((rows_max + mvr::kPrefillBlockRows - 1) / mvr::kPrefillBlockRows);
     const int64_t base_blocks = (int64_t)a->num_seqs * a->num_kv_heads * plan.row_tiles;
@@ -405,7 +405,7 @@ int launch_planned(const mvr_paged_attention_args* a, const mvr::PagedAttentionP
     f.class_q_min = cp.class_q_min;
     f.class_q_max = cp.class_q_max;
     TraceRange launch("attn-prefill-fused");
-    hipError_t err = mvr::launch_paged_prefill(f, a->head_dim, static_cast<hipStream_t>(a->stream));
+    hipError_t err = mvr::launch_paged_prefill(f, a->head_dim, a->dtype == MVR_DTYPE_F32, static_cast<hipStream_t>(a->stream));
     if (err != hipSuccess) return fail(MVR_E_HIP, "kernel launch failed: %s", hipGetErrorString(err));
     return MVR_OK;
   }

@@ -1,4 +1,5 @@
-// Chunked-prefill page-wise attention for gfx950 (F16, MFMA 32x32x16).
+// Chunked-prefill page-wise attention for gfx950 (F16: MFMA 32x32x16; F32:
+// MFMA 32x32x2, see the F32 notes at the products below).
 //
 // Same contract as paged_attention.hip (common.rs:739-817 semantics: grouped
 // rows rho = r*q_len + i, key j visible to query i iff j <= seq_len - q_len + i)
@@ -140,11 +141,13 @@ __device__ __forceinline__ int block_key_tiles(const SeqRows& s, int group_size,
   return last_key < 0 ? 0 : last_key / kTileTokens + 1;
 }
 
-template <int D>
+template <int D, typename T>
 struct Tile {
-  static constexpr int kChunksPerRow = D / 8;                      // 16-byte chunks per token row
-  static constexpr int kChunks = kSuperTokens * kChunksPerRow;     // per K (or V) stage
-  static constexpr int kChunksPerThread = kChunks / (kWaves * 64); // 2 at D=128, 1 at D=64
+  static constexpr bool kF32 = sizeof(T) == 4;
+  static constexpr int kChunkElems = 16 / (int)sizeof(T);            // elements per 16-byte chunk
+  static constexpr int kChunksPerRow = D / kChunkElems;              // 16-byte chunks per token row
+  static constexpr int kChunks = kSuperTokens * kChunksPerRow;       // per K (or V) stage
+  static constexpr int kChunksPerThread = kChunks / (kWaves * 64);   // f16: 2 at D=128, 1 at D=64; f32: 4, 2
   static constexpr int kElems = kSuperTokens * D;
   // V: 32-byte pieces per row, XOR-swizzled with the row.  A transposed read
   // is served per half-wavefront: 4 rows x 2 adjacent pieces, which must land
@@ -152,19 +155,29 @@ struct Tile {
   // pairs apart, measured conflict-free on gfx950 (row&7 cost 2 extra
   // cycles per read).  At D=64 two rows share a 256-byte bank line and
   // row&3 is already conflict-free.
-  __device__ static __forceinline__ int vswz(int t) { return D == 128 ? 2 * (t & 3) : (t & 3); }
-  __device__ static __forceinline__ int kswz(int t) { return t & (kChunksPerRow - 1); }
+  // F32 V rows are not swizzled: each half-wavefront reads one whole token row.
+  __device__ static __forceinline__ int vswz(int t) { return kF32 ? 0 : D == 128 ? 2 * (t & 3) : (t & 3); }
+  // K: the 16 lanes of a ds_read_b128 pass read one chunk of 16 different
+  // rows; XOR with row%16 spreads them over all banks.  Only the low four
+  // chunk bits are swizzled, so at F32 D=128 the upper 16 chunks of a row are
+  // an immediate offset from the lower ones.
+  __device__ static __forceinline__ int kswz(int t) { return t & (kChunksPerRow < 16 ? kChunksPerRow - 1 : 15); }
 };
 
-template <int D>
+template <int D, typename T>
 __global__ __launch_bounds__(kWaves * 64, 1) void paged_prefill_kernel(PrefillParams p) {
-  typedef Tile<D> TL;
+  typedef Tile<D, T> TL;
+  constexpr bool kF32 = TL::kF32;
+  // Q^T fragments (B operand): f16 half8 per 16 dims (32x32x16), f32 float4
+  // per 8 dims (four 32x32x2 products).
+  typedef typename std::conditional<kF32, float4v, half8>::type qfrag_t;
+  constexpr int kQFrags = kF32 ? D / 8 : D / 16;
   // One LDS object per stage and operand: the compiler tracks the
   // direct-to-LDS loads per object, so a read of one stage never waits for
   // the loads still landing in another.
-  __shared__ __attribute__((aligned(16))) half_t k_lds0[TL::kElems], k_lds1[TL::kElems], k_lds2[TL::kElems],
+  __shared__ __attribute__((aligned(16))) T k_lds0[TL::kElems], k_lds1[TL::kElems], k_lds2[TL::kElems],
       k_lds3[TL::kElems];
-  __shared__ __attribute__((aligned(16))) half_t v_lds0[TL::kElems], v_lds1[TL::kElems], v_lds2[TL::kElems],
+  __shared__ __attribute__((aligned(16))) T v_lds0[TL::kElems], v_lds1[TL::kElems], v_lds2[TL::kElems],
       v_lds3[TL::kElems];
   // Group 1 hands its (m, l) to group 0 here after the key loop (its O goes
   // through the then idle stages).
@@ -219,13 +232,16 @@ __global__ __launch_bounds__(kWaves * 64, 1) void paged_prefill_kernel(PrefillPa
   int wave_min_limit = valid ? limit : INT32_MAX;
   for (int off = 1; off < 64; off <<= 1) wave_min_limit = min(wave_min_limit, __shfl_xor(wave_min_limit, off));
 
-  // Q^T as the B operand: lane l holds Q[rho][16s + 8*hh .. +8].
-  half8 q[D / 16];
+  // Q^T as the B operand: lane l holds Q[rho][16s + 8*hh .. +8] (f16) or
+  // Q[rho][8s + 4*hh .. +4] (f32).
+  qfrag_t q[kQFrags];
   {
-    const half_t* qrow = static_cast<const half_t*>(p.q) + (int64_t)(h * p.group_size + r) * p.q_stride_head +
-                         (int64_t)(s.q_start + i) * p.q_stride_token;
+    const T* qrow = static_cast<const T*>(p.q) + (int64_t)(h * p.group_size + r) * p.q_stride_head +
+                    (int64_t)(s.q_start + i) * p.q_stride_token;
+    constexpr int kFragDims = kF32 ? 8 : 16;
 #pragma unroll
-    for (int st = 0; st < D / 16; st++) q[st] = valid ? *reinterpret_cast<const half8*>(qrow + 16 * st + 8 * hh) : half8{};
+    for (int st = 0; st < kQFrags; st++)
+      q[st] = valid ? *reinterpret_cast<const qfrag_t*>(qrow + kFragDims * st + (kFragDims / 2) * hh) : qfrag_t{};
   }
 
   float16v o[D / 32];
@@ -235,8 +251,8 @@ __global__ __launch_bounds__(kWaves * 64, 1) void paged_prefill_kernel(PrefillPa
     for (int e = 0; e < 16; e++) o[n][e] = 0.f;
   float m = -INFINITY, lsum = 0.f;
 
-  const half_t* kpool = static_cast<const half_t*>(p.key_pool);
-  const half_t* vpool = static_cast<const half_t*>(p.value_pool);
+  const T* kpool = static_cast<const T*>(p.key_pool);
+  const T* vpool = static_cast<const T*>(p.value_pool);
   // Block-table reads use the constant address space with a wave-uniform
   // index, so they are scalar loads and never wait on the K/V loads in flight.
   const const_i32* bt = (const const_i32*)(p.block_tables) + (int64_t)b * p.block_table_stride;
@@ -255,24 +271,29 @@ __global__ __launch_bounds__(kWaves * 64, 1) void paged_prefill_kernel(PrefillPa
   // fills LDS chunks (u*8 + w)*64 .. +63 of a stage; LDS chunk P holds token
   // row t = P / (D/8), physical chunk P % (D/8), and the lane fetches the
   // logical 16-byte chunk that the K or V swizzle puts there.  The tokens of
-  // one (w, u) are 4 (D=128) or 8 (D=64) consecutive tokens of a 16-token
-  // group, hence of one page: one scalar block-table load per (w, u).
-  int ld_t[TL::kChunksPerThread], ld_t0[TL::kChunksPerThread], ld_k[TL::kChunksPerThread],
-      ld_v[TL::kChunksPerThread];
+  // one (w, u) are 2 to 8 consecutive tokens (by dtype and head_dim) starting
+  // at a multiple of their count, hence in one page: one scalar block-table
+  // load per (w, u).  The page row of the group's first token goes into the
+  // buffer base each step, so a lane's byte offset within the group never
+  // changes and the loop spends no vector instructions on addresses.
+  int ld_t0[TL::kChunksPerThread];
+  uint32_t off_k[TL::kChunksPerThread], off_v[TL::kChunksPerThread];
 #pragma unroll
   for (int u = 0; u < TL::kChunksPerThread; u++) {
     const int P = (u * kWaves + wave) * 64 + l;
     const int t = P / TL::kChunksPerRow, cs = P % TL::kChunksPerRow;
-    ld_t[u] = t;
     ld_t0[u] = (u * kWaves + wave) * 64 / TL::kChunksPerRow;
-    ld_k[u] = 8 * (cs ^ TL::kswz(t));
-    ld_v[u] = 8 * (2 * ((cs >> 1) ^ TL::vswz(t)) + (cs & 1));
+    const int dt = t - ld_t0[u];
+    off_k[u] = (uint32_t)(dt * D + TL::kChunkElems * (cs ^ TL::kswz(t))) * sizeof(T);
+    off_v[u] = (uint32_t)(dt * D + TL::kChunkElems * (2 * ((cs >> 1) ^ TL::vswz(t)) + (cs & 1))) * sizeof(T);
   }
-  // Branch-free: tokens past the call's last key re-read that key, so every
-  // stage issues the same loads.  Those duplicate keys lie past every row's
-  // causal limit (the last tile is a diagonal tile for every wavefront that
-  // sees it), so their scores are masked to -inf, p = 0, and p * (finite
-  // duplicate V) = 0.  Block-table entries of a stage's (w, u) groups are
+  // Branch-free: every stage issues the same loads.  A group's buffer ends at
+  // the call's last key, so lanes of a group that straddles the end read
+  // zeros (bounds-checked buffer loads return 0), and a stage past the end
+  // re-reads the group holding the last key.  Those tokens lie past every
+  // row's causal limit (the last tile is a diagonal tile for every wavefront
+  // that sees it), so their scores are masked to -inf, p = 0, and p * (zero
+  // or a real V row) = 0.  Block-table entries of a stage's (w, u) groups are
   // read one step before its loads are issued: a scalar load makes its user
   // wait for lgkmcnt(0), which would also drain every LDS read in flight, so
   // the entries are fetched just before a barrier, where lgkmcnt is drained
@@ -289,47 +310,57 @@ __global__ __launch_bounds__(kWaves * 64, 1) void paged_prefill_kernel(PrefillPa
       pr.pg[u] = bt[page_div(min((j0 + 2 * si) * kTileTokens + ld_t0[u], s.key_end - 1))]; // wave-uniform
     return pr;
   };
-  auto issue_stage = [&](int si, const Pages& pages, half_t* kb, half_t* vb) {
+  auto issue_stage = [&](int si, const Pages& pages, T* kb, T* vb) {
 #pragma unroll
     for (int u = 0; u < TL::kChunksPerThread; u++) {
-      const int tg = min((j0 + 2 * si) * kTileTokens + ld_t[u], s.key_end - 1);
-      const int64_t page = (pages.pg[u] * p.num_kv_heads + h) * p.page_size * D; // wave-uniform
-      const uint32_t row = (uint32_t)page_mod(tg) * D;
-      const int dst = (u * kWaves + wave) * 64 * 8;
-      const uint32_t page_bytes = (uint32_t)p.page_size * D * sizeof(half_t);
-      load_page_to_lds16(kpool + page, page_bytes, (row + ld_k[u]) * (uint32_t)sizeof(half_t), kb + dst);
-      load_page_to_lds16(vpool + page, page_bytes, (row + ld_v[u]) * (uint32_t)sizeof(half_t), vb + dst);
+      // All wave-uniform: the group's first token (the last key past the
+      // end), its page row, and the bytes from there to the end of the page
+      // or of the call's keys.
+      const int tc = min((j0 + 2 * si) * kTileTokens + ld_t0[u], s.key_end - 1);
+      const int row0 = page_mod(tc);
+      const int64_t base = ((pages.pg[u] * p.num_kv_heads + h) * p.page_size + row0) * D;
+      const uint32_t bytes = (uint32_t)min(p.page_size - row0, s.key_end - tc) * D * (uint32_t)sizeof(T);
+      const int dst = (u * kWaves + wave) * 64 * TL::kChunkElems;
+      load_page_to_lds16(kpool + base, bytes, off_k[u], kb + dst);
+      load_page_to_lds16(vpool + base, bytes, off_v[u], vb + dst);
     }
   };
   constexpr int kLoadsPerStage = 2 * TL::kChunksPerThread; // per lane
-  half_t* const k_st[4] = {k_lds0, k_lds1, k_lds2, k_lds3};
-  half_t* const v_st[4] = {v_lds0, v_lds1, v_lds2, v_lds3};
+  T* const k_st[4] = {k_lds0, k_lds1, k_lds2, k_lds3};
+  T* const v_st[4] = {v_lds0, v_lds1, v_lds2, v_lds3};
   // O hand-off through the first two K and V stages: part n (16 values per
   // lane) of row wave rw at float (((n * 4 + rw) * 16 + e) * 64 + lane) of
   // their concatenation, 1024 floats per (n, rw).
-  constexpr int kStageFloats = TL::kElems / 2;
+  constexpr int kStageFloats = TL::kElems * (int)sizeof(T) / 4;
   static_assert((D / 32) * kRowWaves * 1024 <= 4 * kStageFloats, "O hand-off exceeds four stages");
   auto xfer_o = [&](int n) -> float* {
     const int f = (n * kRowWaves + rw) * 1024;
     const int obj = f / kStageFloats;
-    half_t* base = obj == 0 ? k_lds0 : obj == 1 ? k_lds1 : obj == 2 ? v_lds0 : v_lds1;
+    T* base = obj == 0 ? k_lds0 : obj == 1 ? k_lds1 : obj == 2 ? v_lds0 : v_lds1;
     return reinterpret_cast<float*>(base) + (f % kStageFloats);
   };
 
   // Per-lane LDS read offsets within this group's 32 rows of a stage.  K:
-  // lane reads token l%32, chunk 2s+hh.  V^T: step u reads rows
-  // 16u+4hh+rsub and +8, 16 columns at 32n+16*(g16&1)+csub, through the
-  // transposing read; rows +8 and +16 keep the same swizzle, so they are
-  // immediate offsets.
+  // lane reads token l%32, chunk 2s+hh (f16: 8 dims per chunk, F32: 4; the
+  // upper 16 chunks of an F32 D=128 row are +64 elements from the lower 16).
+  // V^T (f16): step u reads rows 16u+4hh+rsub and +8, 16 columns at
+  // 32n+16*(g16&1)+csub, through the transposing read; rows +8 and +16 keep
+  // the same swizzle, so they are immediate offsets.  V (F32): lane reads
+  // D/32 consecutive elements (D/32)*(l%32) of row 4hh + 8(e/4) + e%4, all
+  // rows an immediate offset from one base.
   const int gbase = grp * kTileTokens * D;
-  int rk[D / 16];
+  constexpr int kKReads = kF32 ? D / 8 : D / 16; // K fragment reads per tile
+  constexpr int kKOffs = kKReads > 8 ? 8 : kKReads;
+  int rk[kKOffs];
   {
     const int t = l & 31;
 #pragma unroll
-    for (int st = 0; st < D / 16; st++) rk[st] = gbase + t * D + 8 * ((2 * st + hh) ^ TL::kswz(t));
+    for (int st = 0; st < kKOffs; st++) rk[st] = gbase + t * D + TL::kChunkElems * ((2 * st + hh) ^ TL::kswz(t));
   }
-  int rv[D / 32];
-  {
+  int rv[kF32 ? 1 : D / 32];
+  if constexpr (kF32) {
+    rv[0] = gbase + 4 * hh * D + (D / 32) * (l & 31);
+  } else {
     const int g16 = l >> 4, qd = l & 15;
     const int rsub = qd >> 2, csub = 4 * (qd & 3);
 #pragma unroll
@@ -350,14 +381,25 @@ __global__ __launch_bounds__(kWaves * 64, 1) void paged_prefill_kernel(PrefillPa
   auto visible = [&](int j) { return j < j1 && j * kTileTokens <= wave_limit; };
   auto diagonal = [&](int j) { return j * kTileTokens + kTileTokens - 1 > wave_min_limit; };
 
-  // S^T of this group's tile: D/16 MFMAs, K read straight into the A operand.
-  auto qk = [&](const half_t* kb, const int (&rkx)[D / 16]) {
+  // S^T of this group's tile, K read straight into the A operand: f16 D/16
+  // MFMAs 32x32x16; F32 D/2 MFMAs 32x32x2, four per 16-byte K read (product
+  // c pairs dims 8s+c and 8s+4+c across the lane halves, as Q^T does).
+  auto qk = [&](const T* kb, const int (&rkx)[kKOffs]) {
     float16v acc;
 #pragma unroll
     for (int e = 0; e < 16; e++) acc[e] = 0.f;
+    if constexpr (kF32) {
 #pragma unroll
-    for (int st = 0; st < D / 16; st++)
-      acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(*reinterpret_cast<const half8*>(kb + rkx[st]), q[st], acc, 0, 0, 0);
+      for (int st = 0; st < kKReads; st++) {
+        const float4v kf = *reinterpret_cast<const float4v*>(kb + rkx[st % kKOffs] + (st / kKOffs) * 64);
+#pragma unroll
+        for (int c = 0; c < 4; c++) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(kf[c], q[st][c], acc, 0, 0, 0);
+      }
+    } else {
+#pragma unroll
+      for (int st = 0; st < D / 16; st++)
+        acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(*reinterpret_cast<const half8*>(kb + rkx[st]), q[st], acc, 0, 0, 0);
+    }
     return acc;
   };
   // Lane holds tokens tok0 + 8*(e/4) + 4*hh + e%4 of row rho.
@@ -403,7 +445,7 @@ __global__ __launch_bounds__(kWaves * 64, 1) void paged_prefill_kernel(PrefillPa
   };
   // O^T += V^T P^T over two 16-token steps u; step u uses tokens
   // 16u + 4*hh + {0..3} and 16u + 8 + 4*hh + {0..3} (the ones this lane holds).
-  auto pv = [&](const half_t* vb, const int (&rvx)[D / 32], const half8 (&pb)[2]) {
+  auto pv = [&](const T* vb, const int (&rvx)[D / 32], const half8 (&pb)[2]) {
 #pragma unroll
     for (int n = 0; n < D / 32; n++) {
 #pragma unroll
@@ -413,6 +455,30 @@ __global__ __launch_bounds__(kWaves * 64, 1) void paged_prefill_kernel(PrefillPa
         const half8 vt = __builtin_bit_cast(half8, __builtin_shufflevector(ra, rb, 0, 1, 2, 3, 4, 5, 6, 7));
         o[n] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vt, pb[u], o[n], 0, 0, 0);
       }
+    }
+  };
+  // F32: P stays in the S^T registers (exponentials in place) and is the B
+  // operand as it is: product e pairs tokens 8(e/4) + e%4 and +4, which lane
+  // halves 0 and 1 hold in element e.  The A operand is V itself: lane l
+  // takes V[token][(D/32)*(l%32) + n] for product n, so O^T block n holds
+  // dims (D/32)*i + n (i = its row), one 16- or 8-byte read per token pair.
+  auto exps32 = [&](float16v& sv) {
+    const float neg_m = m == -INFINITY ? 0.f : -m;
+    float psum = 0.f;
+#pragma unroll
+    for (int e = 0; e < 16; e++) {
+      sv[e] = __builtin_amdgcn_exp2f(fmaf(sv[e], sl2, neg_m));
+      psum += sv[e];
+    }
+    lsum += psum;
+  };
+  typedef float vrow_t __attribute__((ext_vector_type(D / 32)));
+  auto pv32 = [&](const T* vb, const float16v& pe) {
+#pragma unroll
+    for (int e = 0; e < 16; e++) {
+      const vrow_t vf = *reinterpret_cast<const vrow_t*>(vb + rv[0] + (8 * (e >> 2) + (e & 3)) * D);
+#pragma unroll
+      for (int n = 0; n < D / 32; n++) o[n] = __builtin_amdgcn_mfma_f32_32x32x2f32(vf[n], pe[e], o[n], 0, 0, 0);
     }
   };
 
@@ -425,6 +491,21 @@ __global__ __launch_bounds__(kWaves * 64, 1) void paged_prefill_kernel(PrefillPa
   // fall under group 0's MFMAs, measured slower: 58.4 against 55.7 us.)
   constexpr int kAhead = kStages - 1;                       // steps issued ahead of the one consumed
   constexpr int kInFlight = (kStages - 2) * kLoadsPerStage; // loads a barrier leaves in flight
+  // Every stage starts zeroed: should an out-of-range lane of a direct-to-LDS
+  // load leave its 16 bytes unwritten rather than write the zeros it read,
+  // they hold zeros or an earlier tile's keys, never another kernel's data.
+  // Each lane clears exactly the bytes its own loads fill, and waits for the
+  // stores before issuing them.
+#pragma unroll
+  for (int a = 0; a < kStages; a++) {
+#pragma unroll
+    for (int u = 0; u < TL::kChunksPerThread; u++) {
+      const int e = ((u * kWaves + wave) * 64 + l) * TL::kChunkElems;
+      *reinterpret_cast<u32x4*>(k_st[a] + e) = u32x4{0u, 0u, 0u, 0u};
+      *reinterpret_cast<u32x4*>(v_st[a] + e) = u32x4{0u, 0u, 0u, 0u};
+    }
+  }
+  __builtin_amdgcn_s_waitcnt(0xC07F); // lgkmcnt(0)
 #pragma unroll
   for (int a = 0; a < kAhead; a++) issue_stage(min(a, i_last), fetch_pages(min(a, i_last)), k_st[a], v_st[a]);
   Pages next_pages = fetch_pages(min(kAhead, i_last));
@@ -437,9 +518,14 @@ __global__ __launch_bounds__(kWaves * 64, 1) void paged_prefill_kernel(PrefillPa
     issue_stage(min(si + kAhead, i_last), next_pages, k_st[(st + kAhead) % kStages], v_st[(st + kAhead) % kStages]);
     float16v sc = qk(k_st[st], rk);
     advance_max(row_max(sc));
-    half8 pb[2];
-    exps(sc, pb);
-    pv(v_st[st], rv, pb);
+    if constexpr (kF32) {
+      exps32(sc);
+      pv32(v_st[st], sc);
+    } else {
+      half8 pb[2];
+      exps(sc, pb);
+      pv(v_st[st], rv, pb);
+    }
     next_pages = fetch_pages(min(si + kStages, i_last));
     tile_barrier<kInFlight>();
   };
@@ -451,9 +537,14 @@ __global__ __launch_bounds__(kWaves * 64, 1) void paged_prefill_kernel(PrefillPa
       float16v sc = qk(k_st[st], rk);
       if (diagonal(j)) mask(j, sc);
       advance_max(row_max(sc));
-      half8 pb[2];
-      exps(sc, pb);
-      pv(v_st[st], rv, pb);
+      if constexpr (kF32) {
+        exps32(sc);
+        pv32(v_st[st], sc);
+      } else {
+        half8 pb[2];
+        exps(sc, pb);
+        pv(v_st[st], rv, pb);
+      }
     }
     next_pages = fetch_pages(min(si + kStages, i_last));
     tile_barrier<kInFlight>();
@@ -531,6 +622,36 @@ __global__ __launch_bounds__(kWaves * 64, 1) void paged_prefill_kernel(PrefillPa
   }
 
   const float ltot = lsum + __shfl_xor(lsum, 32);
+  if constexpr (kF32) {
+    // Lane holds O^T[d][rho] for d = (D/32)*(8*(e/4) + 4*hh + e%4) + n.
+    auto put = [&](float* dst, float scale) {
+#pragma unroll
+      for (int e = 0; e < 16; e++) {
+        vrow_t v;
+#pragma unroll
+        for (int n = 0; n < D / 32; n++) v[n] = o[n][e] * scale;
+        *reinterpret_cast<vrow_t*>(dst + (D / 32) * (8 * (e >> 2) + 4 * hh + (e & 3))) = v;
+      }
+    };
+    if (!valid) return;
+    if (p.kv_splits > 1) {
+      const int64_t prow = slot * kBlockRows + rw * kRowsPerWave + (l & 31);
+      put(p.partial_o + prow * D, 1.f);
+      if (hh == 0) {
+        p.partial_ml[prow * 2 + 0] = m;
+        p.partial_ml[prow * 2 + 1] = ltot;
+      }
+    } else if (p.state_o) {
+      const int64_t srow = (int64_t)(h * p.group_size + r) * p.state_tokens + s.q_start + i;
+      put(p.state_o + srow * D, 1.f / ltot);
+      if (hh == 0) p.state_lse[srow] = m + __log2f(ltot);
+    } else {
+      put(static_cast<float*>(p.out) + (int64_t)(h * p.group_size + r) * p.out_stride_head +
+              (int64_t)(s.q_start + i) * p.out_stride_token,
+          1.f / ltot);
+    }
+    return;
+  }
   // Lane holds O^T[d][rho] for d = 32n + 8*(e/4) + 4*hh + e%4.
   if (p.kv_splits == 1) {
     if (valid && p.state_o) {
@@ -580,7 +701,7 @@ __global__ __launch_bounds__(kWaves * 64, 1) void paged_prefill_kernel(PrefillPa
 // lane j holds split j's weight, broadcast by readlane while the partial rows
 // stream as one coalesced 4*D-byte row per load.  Empty splits (no visible
 // key) hold m = -inf, l = 0 and weigh nothing.
-template <int D>
+template <int D, typename T>
 __global__ __launch_bounds__(256) void prefill_merge_kernel(PrefillParams p) {
   constexpr int kPer = D / 64;
   constexpr int kBlocksPerTile = kBlockRows / kMergeWaves;
@@ -625,31 +746,36 @@ __global__ __launch_bounds__(256) void prefill_merge_kernel(PrefillParams p) {
     if (l == 0) p.state_lse[srow] = m_use + __log2f(den);
     return;
   }
-  half_t* dst = static_cast<half_t*>(p.out) + (int64_t)(h * p.group_size + r) * p.out_stride_head +
-                (int64_t)(s.q_start + i) * p.out_stride_token + l * kPer;
+  T* dst = static_cast<T*>(p.out) + (int64_t)(h * p.group_size + r) * p.out_stride_head +
+           (int64_t)(s.q_start + i) * p.out_stride_token + l * kPer;
 #pragma unroll
-  for (int e = 0; e < kPer; e++) dst[e] = (half_t)(acc[e] * inv);
+  for (int e = 0; e < kPer; e++) dst[e] = (T)(acc[e] * inv);
 }
 
-template <int D>
+template <int D, typename T>
 hipError_t launch_typed(const PrefillParams& params, hipStream_t stream) {
   const int pairs = params.num_seqs * params.num_kv_heads;
   const int per_pair = params.row_tiles * params.kv_splits;
   const int64_t blocks =
       pairs >= kXcds ? (int64_t)kXcds * ((pairs + kXcds - 1) / kXcds) * per_pair : (int64_t)pairs * per_pair;
-  hipLaunchKernelGGL(paged_prefill_kernel<D>, dim3((unsigned)blocks), dim3(kWaves * 64), 0, stream, params);
+  hipLaunchKernelGGL((paged_prefill_kernel<D, T>), dim3((unsigned)blocks), dim3(kWaves * 64), 0, stream, params);
   hipError_t err = hipGetLastError();
   if (err != hipSuccess || params.kv_splits == 1) return err;
-  hipLaunchKernelGGL(prefill_merge_kernel<D>, dim3(pairs * params.row_tiles * (kBlockRows / kMergeWaves)), dim3(256), 0,
+  hipLaunchKernelGGL((prefill_merge_kernel<D, T>), dim3(pairs * params.row_tiles * (kBlockRows / kMergeWaves)), dim3(256), 0,
                      stream, params);
   return hipGetLastError();
 }
 
 } // namespace
 
-hipError_t launch_paged_prefill(const PrefillParams& params, int head_dim, hipStream_t stream) {
-  if (head_dim == 128) return launch_typed<128>(params, stream);
-  if (head_dim == 64) return launch_typed<64>(params, stream);
+hipError_t launch_paged_prefill(const PrefillParams& params, int head_dim, bool f32, hipStream_t stream) {
+  if (f32) {
+    if (head_dim == 128) return launch_typed<128, float>(params, stream);
+    if (head_dim == 64) return launch_typed<64, float>(params, stream);
+  } else {
+    if (head_dim == 128) return launch_typed<128, half_t>(params, stream);
+    if (head_dim == 64) return launch_typed<64, half_t>(params, stream);
+  }
   return hipErrorInvalidValue;
 }
 

@@ -39,6 +39,7 @@ struct PrefillParams {
   int32_t class_q_min, class_q_max;
 };
 
-hipError_t launch_paged_prefill(const PrefillParams& params, int head_dim, hipStream_t stream);
+// f32: F32 Q/K/V/out (v_mfma_f32_32x32x2_f32); otherwise F16.
+hipError_t launch_paged_prefill(const PrefillParams& params, int head_dim, bool f32, hipStream_t stream);
 
 } // namespace mvr

@@ -136,7 +136,7 @@ def test_request_level_entry_matches_oracle(dtype, page_size, cached, q_len):
 
 
 @pytest.mark.parametrize("make", [
-    lambda: W.qwen2_7b_chunked_prefill_f16("f32"),        # q_len 256, D 128: 32-row tiles of the split kernel
+    lambda: W.qwen2_7b_chunked_prefill_f16("f32"),        # q_len 256, D 128: the prefill kernel's F32 tile
     lambda: W.llama3_8b_decode_b64_8k_f16(16, "f32"),     # decode, batch 16 x 8K, D 128
 ], ids=["prefill-256-d128", "decode-b16-8k-d128"])
 def test_f32_at_serving_scale_matches_oracle(make):
