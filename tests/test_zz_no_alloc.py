@@ -60,7 +60,18 @@ def test_noalloc_equals_workspace_call_on_consecutive_calls():
     assert torch.equal(n3, r1) and torch.equal(n4, r2)
 
 
-@pytest.mark.parametrize("case", ["repacked-page-size-5", "mixed-with-hints", "block-merge", "prefill-splits"])
+def _long_prefill(dtype):
+    """One 130-token chunk on 4,000 cached tokens, 32/8 heads, D=128: 40 row tiles for 256 CUs, so the prefill
+    kernel splits the keys and merges the splits from fp32 partials in the scratch."""
+    rng = np.random.default_rng(9)
+    lens, qlens = np.array([4130], np.int32), np.array([130], np.int32)
+    n = -(-4130 // 16)
+    bt = rng.permutation(n + 3)[:n].astype(np.int32).reshape(1, n)
+    return W.Workload(f"prefill key splits {dtype}", dtype, 32, 8, 128, 16, n + 3, 0.3, lens, qlens, bt, 9)
+
+
+@pytest.mark.parametrize("case", ["repacked-page-size-5", "mixed-with-hints", "block-merge", "prefill", "prefill-f32",
+                                  "prefill-key-splits-f16", "prefill-key-splits-f32"])
 def test_noalloc_equals_workspace_call_on_every_plan(case):
     if case == "repacked-page-size-5":
         g = torch.Generator(device="cuda").manual_seed(3)
@@ -82,11 +93,16 @@ def test_noalloc_equals_workspace_call_on_every_plan(case):
     elif case == "block-merge":
         w = W.llama3_8b_decode_b64_8k_f16()
         t = W.device_tensors(w, None, seed=6)
+    elif case.startswith("prefill-key-splits"):
+        w = _long_prefill(case.rsplit("-", 1)[1])
+        t = W.device_tensors(w, None, seed=9)
     else:
-        w = W.qwen2_7b_chunked_prefill_f16()
+        w = W.qwen2_7b_chunked_prefill_f16("f32" if case == "prefill-f32" else "f16")
         t = W.device_tensors(w, None, seed=7)
     n, r, need = _both(w, t, hints=(case == "mixed-with-hints"))
     print(f"{case}: scratch {need} bytes", flush=True)
+    if case.startswith("prefill-key-splits"):
+        assert need > 0  # the split partials live in the scratch
     assert torch.equal(n, r)
 
 
