@@ -697,59 +697,85 @@ __global__ __launch_bounds__(kWaves * 64, 1) void paged_prefill_kernel(PrefillPa
 
 // Merges the kv_splits partial results of every block tile:
 //   out = sum_j 2^(m_j - M) o_j / sum_j 2^(m_j - M) l_j.
-// One wavefront per output row (a 256-thread block covers 4 rows of a tile):
-// lane j holds split j's weight, broadcast by readlane while the partial rows
-// stream as one coalesced 4*D-byte row per load.  Empty splits (no visible
-// key) hold m = -inf, l = 0 and weigh nothing.
+// One wavefront per kMergeRows output rows of a tile (a 256-thread block
+// covers 4 x kMergeRows rows): lane j holds split j's weight, broadcast by
+// readlane.  Every split slot's (m, l) and partial row for all of the
+// wavefront's rows are loaded at once, before the rows' bounds are known
+// (the slots exist for all kv_splits <= kMaxSplits; those of splits that did
+// not run are loaded and never used), so the wavefront costs one round trip.
+// Empty splits (no visible key) hold m = -inf, l = 0 and weigh nothing.
+constexpr int kMaxSplits = 8; // the planner's cap on kv_splits
+constexpr int kMergeRows = 4; // output rows per wavefront
 template <int D, typename T>
 __global__ __launch_bounds__(256) void prefill_merge_kernel(PrefillParams p) {
   constexpr int kPer = D / 64;
-  constexpr int kBlocksPerTile = kBlockRows / kMergeWaves;
+  constexpr int kBlocksPerTile = kBlockRows / (kMergeWaves * kMergeRows);
   const int tile = blockIdx.x / kBlocksPerTile; // (b, h, rt)
-  const int lr = (blockIdx.x % kBlocksPerTile) * kMergeWaves + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lr0 = ((blockIdx.x % kBlocksPerTile) * kMergeWaves + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6)) *
+                  kMergeRows;
   const int l = threadIdx.x & 63;
   const int rt = tile % p.row_tiles;
   const int h = (tile / p.row_tiles) % p.num_kv_heads;
   const int b = tile / (p.row_tiles * p.num_kv_heads);
+  const int splits = min(p.kv_splits, kMaxSplits);
+  const int64_t prow0 = (int64_t)tile * p.kv_splits * kBlockRows + lr0; // split j, row r: prow0 + j * kBlockRows + r
+  float mj_raw[kMergeRows], lj_raw[kMergeRows], v[kMergeRows][kMaxSplits][kPer];
+#pragma unroll
+  for (int r = 0; r < kMergeRows; r++) {
+    const int64_t pr = prow0 + (int64_t)l * kBlockRows + r;
+    mj_raw[r] = l < splits ? p.partial_ml[pr * 2] : -INFINITY;
+    lj_raw[r] = l < splits ? p.partial_ml[pr * 2 + 1] : 0.f;
+#pragma unroll
+    for (int j = 0; j < kMaxSplits; j++) {
+      const float* src = p.partial_o + (prow0 + (int64_t)j * kBlockRows + r) * D + l * kPer;
+#pragma unroll
+      for (int e = 0; e < kPer; e++) v[r][j][e] = j < splits ? src[e] : 0.f;
+    }
+  }
   const SeqRows s = load_rows(p, b);
-  const int rho = rt * kBlockRows + lr;
-  if (rho >= p.group_size * s.q_len) return;
+  const int rows = p.group_size * s.q_len;
   const int n_tiles = block_key_tiles(s, p.group_size, rt);
   if (n_tiles == 0) return;
   const int tiles_per_split = (n_tiles + p.kv_splits - 1) / p.kv_splits;
-  const int n_parts = (n_tiles + tiles_per_split - 1) / tiles_per_split; // splits that ran (<= 8 < 64 lanes)
-  const int64_t prow0 = (int64_t)tile * p.kv_splits * kBlockRows + lr;  // split j: prow0 + j * kBlockRows
-  const float mj = l < n_parts ? p.partial_ml[(prow0 + (int64_t)l * kBlockRows) * 2] : -INFINITY;
-  float mmax = mj;
+  const int n_parts = min((n_tiles + tiles_per_split - 1) / tiles_per_split, splits); // splits that ran
 #pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) mmax = fmaxf(mmax, __shfl_xor(mmax, off));
-  const float m_use = mmax == -INFINITY ? 0.f : mmax;
-  const float w = mj == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mj - m_use);
-  float den = l < n_parts ? w * p.partial_ml[(prow0 + (int64_t)l * kBlockRows) * 2 + 1] : 0.f;
+  for (int r = 0; r < kMergeRows; r++) {
+    const int rho = rt * kBlockRows + lr0 + r;
+    if (rho >= rows) break;
+    const float mj = l < n_parts ? mj_raw[r] : -INFINITY;
+    float mmax = mj;
 #pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) den += __shfl_xor(den, off);
-  float acc[kPer];
+    for (int off = 32; off >= 1; off >>= 1) mmax = fmaxf(mmax, __shfl_xor(mmax, off));
+    const float m_use = mmax == -INFINITY ? 0.f : mmax;
+    const float w = mj == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mj - m_use);
+    float den = l < n_parts ? w * lj_raw[r] : 0.f;
 #pragma unroll
-  for (int e = 0; e < kPer; e++) acc[e] = 0.f;
-  for (int j = 0; j < n_parts; j++) {
-    const float wj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), j));
-    const float* src = p.partial_o + (prow0 + (int64_t)j * kBlockRows) * D + l * kPer;
+    for (int off = 32; off >= 1; off >>= 1) den += __shfl_xor(den, off);
+    float acc[kPer];
 #pragma unroll
-    for (int e = 0; e < kPer; e++) acc[e] = fmaf(wj, src[e], acc[e]);
+    for (int e = 0; e < kPer; e++) acc[e] = 0.f;
+#pragma unroll
+    for (int j = 0; j < kMaxSplits; j++) {
+      if (j < n_parts) {
+        const float wj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), j));
+#pragma unroll
+        for (int e = 0; e < kPer; e++) acc[e] = fmaf(wj, v[r][j][e], acc[e]);
+      }
+    }
+    const int qr = rho / s.q_len, i = rho % s.q_len;
+    const float inv = 1.f / den;
+    if (p.state_o) {
+      const int64_t srow = (int64_t)(h * p.group_size + qr) * p.state_tokens + s.q_start + i;
+#pragma unroll
+      for (int e = 0; e < kPer; e++) p.state_o[srow * D + l * kPer + e] = acc[e] * inv;
+      if (l == 0) p.state_lse[srow] = m_use + __log2f(den);
+      continue;
+    }
+    T* dst = static_cast<T*>(p.out) + (int64_t)(h * p.group_size + qr) * p.out_stride_head +
+             (int64_t)(s.q_start + i) * p.out_stride_token + l * kPer;
+#pragma unroll
+    for (int e = 0; e < kPer; e++) dst[e] = (T)(acc[e] * inv);
   }
-  const int r = rho / s.q_len, i = rho % s.q_len;
-  const float inv = 1.f / den;
-  if (p.state_o) {
-    const int64_t srow = (int64_t)(h * p.group_size + r) * p.state_tokens + s.q_start + i;
-#pragma unroll
-    for (int e = 0; e < kPer; e++) p.state_o[srow * D + l * kPer + e] = acc[e] * inv;
-    if (l == 0) p.state_lse[srow] = m_use + __log2f(den);
-    return;
-  }
-  T* dst = static_cast<T*>(p.out) + (int64_t)(h * p.group_size + r) * p.out_stride_head +
-           (int64_t)(s.q_start + i) * p.out_stride_token + l * kPer;
-#pragma unroll
-  for (int e = 0; e < kPer; e++) dst[e] = (T)(acc[e] * inv);
 }
 
 template <int D, typename T>
@@ -761,7 +787,7 @@ hipError_t launch_typed(const PrefillParams& params, hipStream_t stream) {
   hipLaunchKernelGGL((paged_prefill_kernel<D, T>), dim3((unsigned)blocks), dim3(kWaves * 64), 0, stream, params);
   hipError_t err = hipGetLastError();
   if (err != hipSuccess || params.kv_splits == 1) return err;
-  hipLaunchKernelGGL((prefill_merge_kernel<D, T>), dim3(pairs * params.row_tiles * (kBlockRows / kMergeWaves)), dim3(256), 0,
+  hipLaunchKernelGGL((prefill_merge_kernel<D, T>), dim3(pairs * params.row_tiles * (kBlockRows / (kMergeWaves * kMergeRows))), dim3(256), 0,
                      stream, params);
   return hipGetLastError();
 }
