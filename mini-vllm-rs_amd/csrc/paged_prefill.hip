@@ -697,18 +697,26 @@ __global__ __launch_bounds__(kWaves * 64, 1) void paged_prefill_kernel(PrefillPa
 
 // Merges the kv_splits partial results of every block tile:
 //   out = sum_j 2^(m_j - M) o_j / sum_j 2^(m_j - M) l_j.
-// One wavefront per kMergeRows output rows of a tile (a 256-thread block
-// covers 4 x kMergeRows rows): lane j holds split j's weight, broadcast by
-// readlane.  Every split slot's (m, l) and partial row for all of the
+// One wavefront per merge_rows<D>() output rows of a tile (a 256-thread
+// block covers 4 x that many rows): lane j holds split j's weight, broadcast
+// by readlane.  Every split slot's (m, l) and partial row for all of the
 // wavefront's rows are loaded at once, before the rows' bounds are known
 // (the slots exist for all kv_splits <= kMaxSplits; those of splits that did
 // not run are loaded and never used), so the wavefront costs one round trip.
 // Empty splits (no visible key) hold m = -inf, l = 0 and weigh nothing.
 constexpr int kMaxSplits = 8; // the planner's cap on kv_splits
-constexpr int kMergeRows = 4; // output rows per wavefront
+// Output rows per wavefront.  Measured on key-split prefill calls: at D=64 (one
+// element per lane) two rows per wavefront took a Qwen2-0.5B-shape chunk from
+// 34.5 to 32.5 us; at D=128 two or four rows slowed the shared-prompt
+// cascade's prefix pass by 1-4 us, so it keeps one.
+template <int D>
+constexpr int merge_rows() {
+  return D == 64 ? 2 : 1;
+}
 template <int D, typename T>
 __global__ __launch_bounds__(256) void prefill_merge_kernel(PrefillParams p) {
   constexpr int kPer = D / 64;
+  constexpr int kMergeRows = merge_rows<D>();
   constexpr int kBlocksPerTile = kBlockRows / (kMergeWaves * kMergeRows);
   const int tile = blockIdx.x / kBlocksPerTile; // (b, h, rt)
   const int lr0 = ((blockIdx.x % kBlocksPerTile) * kMergeWaves + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6)) *
@@ -787,7 +795,8 @@ hipError_t launch_typed(const PrefillParams& params, hipStream_t stream) {
   hipLaunchKernelGGL((paged_prefill_kernel<D, T>), dim3((unsigned)blocks), dim3(kWaves * 64), 0, stream, params);
   hipError_t err = hipGetLastError();
   if (err != hipSuccess || params.kv_splits == 1) return err;
-  hipLaunchKernelGGL((prefill_merge_kernel<D, T>), dim3(pairs * params.row_tiles * (kBlockRows / (kMergeWaves * kMergeRows))), dim3(256), 0,
+  hipLaunchKernelGGL((prefill_merge_kernel<D, T>), dim3(pairs * params.row_tiles * (kBlockRows / (kMergeWaves * merge_rows<D>()))),
+                     dim3(256), 0,
                      stream, params);
   return hipGetLastError();
 }
