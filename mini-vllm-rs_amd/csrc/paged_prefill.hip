@@ -9,16 +9,17 @@
 //
 // Block = 8 wavefronts over 128 consecutive grouped rows of one (sequence, KV
 // head): two groups of 4 wavefronts (32 rows each) hold the same rows and
-// take alternating 32-token key tiles, so every SIMD runs two wavefronts
-// without splitting the keys across blocks; at the end group 1 hands its
-// (O, m, l) to group 0 through LDS and group 0 merges and writes.  Each step
-// stages 64 tokens (one tile per group) in LDS through a ring of kStages
-// stages filled by direct-to-LDS loads (16 KiB of K and of V per stage at
-// D=128):
+// take alternating key tiles (TT = 64 tokens for F16, 32 for F32), so every
+// SIMD runs two wavefronts without splitting the keys across blocks; at the
+// end group 1 hands its (O, m, l) to group 0 through LDS and group 0 merges
+// and writes.  Each step stages 2 TT tokens (one tile per group) in LDS
+// through a ring of kStages stages filled by direct-to-LDS loads (32 KiB of K
+// and of V per stage at D=128 F16):
 //   * K tile: 16-byte chunks, XOR swizzle (chunk ^ row%16), read back with
 //     ds_read_b128 in the v_mfma_f32_32x32x16_f16 A-operand layout
-//     (lane l: token l%32, dims 8*(l/32)+16s);  S^T = K Q^T in D/16 MFMAs;
-//   * S^T lands with lane l owning row l%32 and 16 tokens; the online softmax
+//     (lane l: token l%32, dims 8*(l/32)+16s);  S^T = K Q^T in D/16 MFMAs
+//     per 32 tokens of the tile;
+//   * S^T lands with lane l owning row l%32 and 16 tokens per 32; the online softmax
 //     is exp2-based with a lazy rescale: the running max only moves (and O is
 //     only rescaled) when a score exceeds it by more than 2^8;
 //   * V tile: 32-byte-piece swizzle, ds_read_b64_tr_b16 twice per operand
@@ -48,19 +49,17 @@ typedef __attribute__((address_space(3))) short4v lds_short4;
 typedef __attribute__((address_space(3))) void lds_void;
 typedef __attribute__((address_space(4))) int32_t const_i32;
 
-constexpr int kTileTokens = 32;
 constexpr int kRowsPerWave = 32;
 constexpr int kRowWaves = 4;                        // wavefronts per 128-row group
 constexpr int kGroups = 2;                          // wavefront groups taking alternating key tiles
 constexpr int kWaves = kRowWaves * kGroups;         // wavefronts per block
-constexpr int kSuperTokens = kTileTokens * kGroups; // tokens per LDS stage: one tile per group
 constexpr int kBlockRows = kRowsPerWave * kRowWaves;
 constexpr int kMergeWaves = 4; // wavefronts per block of prefill_merge_kernel
 constexpr int kXcds = 8;
 #ifndef MVR_PREFILL_STAGES
 #define MVR_PREFILL_STAGES 2
 #endif
-// LDS stages of kSuperTokens tokens (2, 3 or 4; the unrolled loop names each
+// LDS stages of one key tile per group (2, 3 or 4; the unrolled loop names each
 // statically).  Measured on the Qwen2-7B prefill chunk: 2, 3 and 4 stages
 // within 1%: the step's loads land under the step's compute.
 constexpr int kStages = MVR_PREFILL_STAGES;
@@ -130,7 +129,9 @@ __device__ __forceinline__ SeqRows load_rows(const PrefillParams& p, int b) {
 // Causal limit of query i within this call's keys (common.rs:948-965).
 __device__ __forceinline__ int row_limit(const SeqRows& s, int i) { return min(s.seq_len - s.q_len + i, s.key_end - 1); }
 
-// Keys the block's rows can see: up to the largest causal limit among them.
+// Key tiles of TT tokens the block's rows can see: up to the largest causal
+// limit among them.
+template <int TT>
 __device__ __forceinline__ int block_key_tiles(const SeqRows& s, int group_size, int rt) {
   const int rows = group_size * s.q_len;
   const int rho0 = rt * kBlockRows;
@@ -138,11 +139,12 @@ __device__ __forceinline__ int block_key_tiles(const SeqRows& s, int group_size,
   const int rho1 = min(rho0 + kBlockRows, rows) - 1;
   const int max_i = (rho1 / s.q_len != rho0 / s.q_len) ? s.q_len - 1 : rho1 % s.q_len;
   const int last_key = row_limit(s, max_i); // -1: no key (a prefix pass over an empty prefix)
-  return last_key < 0 ? 0 : last_key / kTileTokens + 1;
+  return last_key < 0 ? 0 : last_key / TT + 1;
 }
 
-template <int D, typename T>
+template <int D, typename T, int TT>
 struct Tile {
+  static constexpr int kSuperTokens = TT * kGroups; // tokens per LDS stage: one tile per group
   static constexpr bool kF32 = sizeof(T) == 4;
   static constexpr int kChunkElems = 16 / (int)sizeof(T);            // elements per 16-byte chunk
   static constexpr int kChunksPerRow = D / kChunkElems;              // 16-byte chunks per token row
@@ -164,10 +166,14 @@ struct Tile {
   __device__ static __forceinline__ int kswz(int t) { return t & (kChunksPerRow < 16 ? kChunksPerRow - 1 : 15); }
 };
 
-template <int D, typename T>
+template <int D, typename T, int TT>
 __global__ __launch_bounds__(kWaves * 64, 1) void paged_prefill_kernel(PrefillParams p) {
-  typedef Tile<D, T> TL;
+  typedef Tile<D, T, TT> TL;
   constexpr bool kF32 = TL::kF32;
+  // Key tile of one group per step: TT tokens = kSub S^T blocks of 32 tokens.
+  constexpr int kTileTokens = TT;
+  constexpr int kSub = TT / 32;
+  static_assert(TT == 32 || (TT == 64 && !kF32), "32-token tiles, or 64 for F16");
   // Q^T fragments (B operand): f16 half8 per 16 dims (32x32x16), f32 float4
   // per 8 dims (four 32x32x2 products).
   typedef typename std::conditional<kF32, float4v, half8>::type qfrag_t;
@@ -213,7 +219,7 @@ __global__ __launch_bounds__(kWaves * 64, 1) void paged_prefill_kernel(PrefillPa
 
   const SeqRows s = load_rows(p, b);
   const int rows = p.group_size * s.q_len;
-  const int n_tiles = block_key_tiles(s, p.group_size, rt);
+  const int n_tiles = block_key_tiles<TT>(s, p.group_size, rt);
   if (n_tiles == 0) return; // whole block: uniform exit before any barrier
   const int tiles_per_split = (n_tiles + p.kv_splits - 1) / p.kv_splits;
   const int j0 = split * tiles_per_split;
@@ -263,8 +269,8 @@ __global__ __launch_bounds__(kWaves * 64, 1) void paged_prefill_kernel(PrefillPa
   auto page_div = [&](int tok) { return tok >> pshift; };
   auto page_mod = [&](int tok) { return tok & (p.page_size - 1); };
 
-  // A stage holds the 64 tokens of one step: tile j0 + 2i (group 0) in rows
-  // 0..31 and tile j0 + 2i + 1 (group 1) in rows 32..63.  Tokens move
+  // A stage holds the 2 TT tokens of one step: tile j0 + 2i (group 0) in rows
+  // 0..TT-1 and tile j0 + 2i + 1 (group 1) in rows TT..2TT-1.  Tokens move
   // straight from HBM/L2 into LDS (buffer_load_dwordx4 ... lds: lane i of a
   // wavefront writes 16 bytes at the wavefront's LDS base + 16 i), so they
   // take no registers and no LDS store instructions.  Wavefront w, step u
@@ -384,37 +390,51 @@ __global__ __launch_bounds__(kWaves * 64, 1) void paged_prefill_kernel(PrefillPa
   // S^T of this group's tile, K read straight into the A operand: f16 D/16
   // MFMAs 32x32x16; F32 D/2 MFMAs 32x32x2, four per 16-byte K read (product
   // c pairs dims 8s+c and 8s+4+c across the lane halves, as Q^T does).
-  auto qk = [&](const T* kb, const int (&rkx)[kKOffs]) {
-    float16v acc;
+  // (F16, TT = 64: the tile's two 32-token S^T blocks, their products
+  // interleaved so that the two accumulation chains overlap.)
+  auto qk = [&](const T* kb, const int (&rkx)[kKOffs], float16v (&acc)[kSub]) {
 #pragma unroll
-    for (int e = 0; e < 16; e++) acc[e] = 0.f;
+    for (int c = 0; c < kSub; c++)
+#pragma unroll
+      for (int e = 0; e < 16; e++) acc[c][e] = 0.f;
     if constexpr (kF32) {
 #pragma unroll
       for (int st = 0; st < kKReads; st++) {
         const float4v kf = *reinterpret_cast<const float4v*>(kb + rkx[st % kKOffs] + (st / kKOffs) * 64);
 #pragma unroll
-        for (int c = 0; c < 4; c++) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(kf[c], q[st][c], acc, 0, 0, 0);
+        for (int c = 0; c < 4; c++) acc[0] = __builtin_amdgcn_mfma_f32_32x32x2f32(kf[c], q[st][c], acc[0], 0, 0, 0);
       }
     } else {
 #pragma unroll
       for (int st = 0; st < D / 16; st++)
-        acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(*reinterpret_cast<const half8*>(kb + rkx[st]), q[st], acc, 0, 0, 0);
-    }
-    return acc;
-  };
-  // Lane holds tokens tok0 + 8*(e/4) + 4*hh + e%4 of row rho.
-  auto mask = [&](int j, float16v& sv) {
-    const int rel = limit - j * kTileTokens - 4 * hh;
 #pragma unroll
-    for (int e = 0; e < 16; e++) sv[e] = 8 * (e >> 2) + (e & 3) <= rel ? sv[e] : -INFINITY;
+        for (int c = 0; c < kSub; c++)
+          acc[c] = __builtin_amdgcn_mfma_f32_32x32x16_f16(*reinterpret_cast<const half8*>(kb + rkx[st] + 32 * c * D), q[st],
+                                                          acc[c], 0, 0, 0);
+    }
+  };
+  // In block c the lane holds tokens tok0 + 32c + 8*(e/4) + 4*hh + e%4 of row rho.
+  auto mask = [&](int j, float16v (&sv)[kSub]) {
+#pragma unroll
+    for (int c = 0; c < kSub; c++) {
+      const int rel = limit - j * kTileTokens - 32 * c - 4 * hh;
+#pragma unroll
+      for (int e = 0; e < 16; e++) sv[c][e] = 8 * (e >> 2) + (e & 3) <= rel ? sv[c][e] : -INFINITY;
+    }
   };
   // Scaled row max (log2 units; scale > 0 keeps the order), both lane halves.
-  auto row_max = [&](const float16v& sv) {
-    float a = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
-    float bb = fmaxf(fmaxf(sv[4], sv[5]), fmaxf(sv[6], sv[7]));
-    float c = fmaxf(fmaxf(sv[8], sv[9]), fmaxf(sv[10], sv[11]));
-    float d = fmaxf(fmaxf(sv[12], sv[13]), fmaxf(sv[14], sv[15]));
-    const float mx = fmaxf(fmaxf(a, bb), fmaxf(c, d)) * sl2;
+  auto row_max = [&](const float16v (&svs)[kSub]) {
+    float mxs = -INFINITY;
+#pragma unroll
+    for (int c = 0; c < kSub; c++) {
+      const float16v& sv = svs[c];
+      float a = fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]));
+      float bb = fmaxf(fmaxf(sv[4], sv[5]), fmaxf(sv[6], sv[7]));
+      float cc = fmaxf(fmaxf(sv[8], sv[9]), fmaxf(sv[10], sv[11]));
+      float d = fmaxf(fmaxf(sv[12], sv[13]), fmaxf(sv[14], sv[15]));
+      mxs = c == 0 ? fmaxf(fmaxf(a, bb), fmaxf(cc, d)) : fmaxf(mxs, fmaxf(fmaxf(a, bb), fmaxf(cc, d)));
+    }
+    const float mx = mxs * sl2;
     const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx), false, false);
     return fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
   };
@@ -432,24 +452,26 @@ __global__ __launch_bounds__(kWaves * 64, 1) void paged_prefill_kernel(PrefillPa
     }
   };
   // P = 2^(s*scale_log2 - m) in f16 (masked keys give 2^-inf = 0) and its row sum.
-  auto exps = [&](const float16v& sv, half8 (&pb)[2]) {
+  auto exps = [&](const float16v (&sv)[kSub], half8 (&pb)[2 * kSub]) {
     const float neg_m = m == -INFINITY ? 0.f : -m;
     float psum = 0.f;
 #pragma unroll
-    for (int e = 0; e < 16; e++) {
-      const float pe = __builtin_amdgcn_exp2f(fmaf(sv[e], sl2, neg_m));
-      psum += pe;
-      pb[e >> 3][e & 7] = (half_t)pe;
-    }
+    for (int c = 0; c < kSub; c++)
+#pragma unroll
+      for (int e = 0; e < 16; e++) {
+        const float pe = __builtin_amdgcn_exp2f(fmaf(sv[c][e], sl2, neg_m));
+        psum += pe;
+        pb[2 * c + (e >> 3)][e & 7] = (half_t)pe;
+      }
     lsum += psum;
   };
-  // O^T += V^T P^T over two 16-token steps u; step u uses tokens
+  // O^T += V^T P^T over the tile's 16-token steps u; step u uses tokens
   // 16u + 4*hh + {0..3} and 16u + 8 + 4*hh + {0..3} (the ones this lane holds).
-  auto pv = [&](const T* vb, const int (&rvx)[D / 32], const half8 (&pb)[2]) {
+  auto pv = [&](const T* vb, const int (&rvx)[D / 32], const half8 (&pb)[2 * kSub]) {
 #pragma unroll
     for (int n = 0; n < D / 32; n++) {
 #pragma unroll
-      for (int u = 0; u < 2; u++) {
+      for (int u = 0; u < 2 * kSub; u++) {
         const short4v ra = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4*)(vb + rvx[n] + 16 * D * u));
         const short4v rb = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4*)(vb + rvx[n] + 16 * D * u + 8 * D));
         const half8 vt = __builtin_bit_cast(half8, __builtin_shufflevector(ra, rb, 0, 1, 2, 3, 4, 5, 6, 7));
@@ -516,13 +538,14 @@ __global__ __launch_bounds__(kWaves * 64, 1) void paged_prefill_kernel(PrefillPa
   auto step_clear = [&](int si, auto st_c) {
     constexpr int st = decltype(st_c)::value;
     issue_stage(min(si + kAhead, i_last), next_pages, k_st[(st + kAhead) % kStages], v_st[(st + kAhead) % kStages]);
-    float16v sc = qk(k_st[st], rk);
+    float16v sc[kSub];
+    qk(k_st[st], rk, sc);
     advance_max(row_max(sc));
     if constexpr (kF32) {
-      exps32(sc);
-      pv32(v_st[st], sc);
+      exps32(sc[0]);
+      pv32(v_st[st], sc[0]);
     } else {
-      half8 pb[2];
+      half8 pb[2 * kSub];
       exps(sc, pb);
       pv(v_st[st], rv, pb);
     }
@@ -534,14 +557,15 @@ __global__ __launch_bounds__(kWaves * 64, 1) void paged_prefill_kernel(PrefillPa
     issue_stage(min(si + kAhead, i_last), next_pages, k_st[(st + kAhead) % kStages], v_st[(st + kAhead) % kStages]);
     const int j = j0 + 2 * si + grp;
     if (visible(j)) {
-      float16v sc = qk(k_st[st], rk);
+      float16v sc[kSub];
+      qk(k_st[st], rk, sc);
       if (diagonal(j)) mask(j, sc);
       advance_max(row_max(sc));
       if constexpr (kF32) {
-        exps32(sc);
-        pv32(v_st[st], sc);
+        exps32(sc[0]);
+        pv32(v_st[st], sc[0]);
       } else {
-        half8 pb[2];
+        half8 pb[2 * kSub];
         exps(sc, pb);
         pv(v_st[st], rv, pb);
       }
@@ -713,7 +737,7 @@ template <int D>
 constexpr int merge_rows() {
   return D == 64 ? 2 : 1;
 }
-template <int D, typename T>
+template <int D, typename T, int TT>
 __global__ __launch_bounds__(256) void prefill_merge_kernel(PrefillParams p) {
   constexpr int kPer = D / 64;
   constexpr int kMergeRows = merge_rows<D>();
@@ -742,7 +766,7 @@ __global__ __launch_bounds__(256) void prefill_merge_kernel(PrefillParams p) {
   }
   const SeqRows s = load_rows(p, b);
   const int rows = p.group_size * s.q_len;
-  const int n_tiles = block_key_tiles(s, p.group_size, rt);
+  const int n_tiles = block_key_tiles<TT>(s, p.group_size, rt);
   if (n_tiles == 0) return;
   const int tiles_per_split = (n_tiles + p.kv_splits - 1) / p.kv_splits;
   const int n_parts = min((n_tiles + tiles_per_split - 1) / tiles_per_split, splits); // splits that ran
@@ -786,16 +810,21 @@ __global__ __launch_bounds__(256) void prefill_merge_kernel(PrefillParams p) {
   }
 }
 
+// Key tile per group and step: 64 tokens for F16 (the per-tile row max,
+// rescale test, barrier and block-table work spread over twice the keys:
+// 48.8 -> 47.0 us on the Qwen2-7B chunk, 32.3 -> 31.5 us on a Qwen2-0.5B-shape
+// chunk), 32 for F32, whose 64-token stages would not fit in LDS.
 template <int D, typename T>
 hipError_t launch_typed(const PrefillParams& params, hipStream_t stream) {
+  constexpr int TT = sizeof(T) == 4 ? 32 : 64;
   const int pairs = params.num_seqs * params.num_kv_heads;
   const int per_pair = params.row_tiles * params.kv_splits;
   const int64_t blocks =
       pairs >= kXcds ? (int64_t)kXcds * ((pairs + kXcds - 1) / kXcds) * per_pair : (int64_t)pairs * per_pair;
-  hipLaunchKernelGGL((paged_prefill_kernel<D, T>), dim3((unsigned)blocks), dim3(kWaves * 64), 0, stream, params);
+  hipLaunchKernelGGL((paged_prefill_kernel<D, T, TT>), dim3((unsigned)blocks), dim3(kWaves * 64), 0, stream, params);
   hipError_t err = hipGetLastError();
   if (err != hipSuccess || params.kv_splits == 1) return err;
-  hipLaunchKernelGGL((prefill_merge_kernel<D, T>), dim3(pairs * params.row_tiles * (kBlockRows / (kMergeWaves * merge_rows<D>()))),
+  hipLaunchKernelGGL((prefill_merge_kernel<D, T, TT>), dim3(pairs * params.row_tiles * (kBlockRows / (kMergeWaves * merge_rows<D>()))),
                      dim3(256), 0,
                      stream, params);
   return hipGetLastError();
