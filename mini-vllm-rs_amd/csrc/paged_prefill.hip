@@ -273,23 +273,25 @@ __global__ __launch_bounds__(kWaves * 64, 1) void paged_prefill_kernel(PrefillPa
   // 0..TT-1 and tile j0 + 2i + 1 (group 1) in rows TT..2TT-1.  Tokens move
   // straight from HBM/L2 into LDS (buffer_load_dwordx4 ... lds: lane i of a
   // wavefront writes 16 bytes at the wavefront's LDS base + 16 i), so they
-  // take no registers and no LDS store instructions.  Wavefront w, step u
-  // fills LDS chunks (u*8 + w)*64 .. +63 of a stage; LDS chunk P holds token
-  // row t = P / (D/8), physical chunk P % (D/8), and the lane fetches the
-  // logical 16-byte chunk that the K or V swizzle puts there.  The tokens of
-  // one (w, u) are 2 to 8 consecutive tokens (by dtype and head_dim) starting
-  // at a multiple of their count, hence in one page: one scalar block-table
-  // load per (w, u).  The page row of the group's first token goes into the
-  // buffer base each step, so a lane's byte offset within the group never
-  // changes and the loop spends no vector instructions on addresses.
-  int ld_t0[TL::kChunksPerThread];
+  // take no registers and no LDS store instructions.  Wavefront w fills the
+  // stage's rows w*R .. w*R+R-1 (R = 2 TT / 8 tokens: 16 for F16, 8 for F32),
+  // its load u LDS chunks (w*kChunksPerThread + u)*64 .. +63; LDS chunk P
+  // holds token row t = P / (D/8), physical chunk P % (D/8), and the lane
+  // fetches the logical 16-byte chunk that the K or V swizzle puts there.  A
+  // wavefront's R tokens are consecutive and start at a multiple of R, hence
+  // lie in one page (page sizes here are powers of two, at least 16): one
+  // scalar block-table load, one page address and one bound per wavefront
+  // and step.  That page row goes into the buffer base, so a lane's byte
+  // offset within the wavefront's tokens never changes and the loop spends no
+  // vector instructions on addresses.
+  constexpr int kWaveTokens = TL::kChunksPerThread * 64 / TL::kChunksPerRow; // R
+  const int ld_t0 = wave * kWaveTokens;
   uint32_t off_k[TL::kChunksPerThread], off_v[TL::kChunksPerThread];
 #pragma unroll
   for (int u = 0; u < TL::kChunksPerThread; u++) {
-    const int P = (u * kWaves + wave) * 64 + l;
+    const int P = (wave * TL::kChunksPerThread + u) * 64 + l;
     const int t = P / TL::kChunksPerRow, cs = P % TL::kChunksPerRow;
-    ld_t0[u] = (u * kWaves + wave) * 64 / TL::kChunksPerRow;
-    const int dt = t - ld_t0[u];
+    const int dt = t - ld_t0;
     off_k[u] = (uint32_t)(dt * D + TL::kChunkElems * (cs ^ TL::kswz(t))) * sizeof(T);
     off_v[u] = (uint32_t)(dt * D + TL::kChunkElems * (2 * ((cs >> 1) ^ TL::vswz(t)) + (cs & 1))) * sizeof(T);
   }
@@ -299,7 +301,7 @@ __global__ __launch_bounds__(kWaves * 64, 1) void paged_prefill_kernel(PrefillPa
   // re-reads the group holding the last key.  Those tokens lie past every
   // row's causal limit (the last tile is a diagonal tile for every wavefront
   // that sees it), so their scores are masked to -inf, p = 0, and p * (zero
-  // or a real V row) = 0.  Block-table entries of a stage's (w, u) groups are
+  // or a real V row) = 0.  A wavefront's block-table entry for a stage is
   // read one step before its loads are issued: a scalar load makes its user
   // wait for lgkmcnt(0), which would also drain every LDS read in flight, so
   // the entries are fetched just before a barrier, where lgkmcnt is drained
@@ -307,26 +309,22 @@ __global__ __launch_bounds__(kWaves * 64, 1) void paged_prefill_kernel(PrefillPa
   const int n_steps = (j1 - j0 + 1) / 2;
   const int i_last = max(n_steps - 1, 0);
   struct Pages {
-    int64_t pg[TL::kChunksPerThread];
+    int64_t pg;
   };
   auto fetch_pages = [&](int si) {
-    Pages pr;
-#pragma unroll
-    for (int u = 0; u < TL::kChunksPerThread; u++)
-      pr.pg[u] = bt[page_div(min((j0 + 2 * si) * kTileTokens + ld_t0[u], s.key_end - 1))]; // wave-uniform
-    return pr;
+    return Pages{bt[page_div(min((j0 + 2 * si) * kTileTokens + ld_t0, s.key_end - 1))]}; // wave-uniform
   };
   auto issue_stage = [&](int si, const Pages& pages, T* kb, T* vb) {
+    // All wave-uniform: the wavefront's first token (the last key past the
+    // end), its page row, and the bytes from there to the end of the page or
+    // of the call's keys.
+    const int tc = min((j0 + 2 * si) * kTileTokens + ld_t0, s.key_end - 1);
+    const int row0 = page_mod(tc);
+    const int64_t base = ((pages.pg * p.num_kv_heads + h) * p.page_size + row0) * D;
+    const uint32_t bytes = (uint32_t)min(p.page_size - row0, s.key_end - tc) * D * (uint32_t)sizeof(T);
 #pragma unroll
     for (int u = 0; u < TL::kChunksPerThread; u++) {
-      // All wave-uniform: the group's first token (the last key past the
-      // end), its page row, and the bytes from there to the end of the page
-      // or of the call's keys.
-      const int tc = min((j0 + 2 * si) * kTileTokens + ld_t0[u], s.key_end - 1);
-      const int row0 = page_mod(tc);
-      const int64_t base = ((pages.pg[u] * p.num_kv_heads + h) * p.page_size + row0) * D;
-      const uint32_t bytes = (uint32_t)min(p.page_size - row0, s.key_end - tc) * D * (uint32_t)sizeof(T);
-      const int dst = (u * kWaves + wave) * 64 * TL::kChunkElems;
+      const int dst = (wave * TL::kChunksPerThread + u) * 64 * TL::kChunkElems;
       load_page_to_lds16(kpool + base, bytes, off_k[u], kb + dst);
       load_page_to_lds16(vpool + base, bytes, off_v[u], vb + dst);
     }
@@ -522,7 +520,7 @@ __global__ __launch_bounds__(kWaves * 64, 1) void paged_prefill_kernel(PrefillPa
   for (int a = 0; a < kStages; a++) {
 #pragma unroll
     for (int u = 0; u < TL::kChunksPerThread; u++) {
-      const int e = ((u * kWaves + wave) * 64 + l) * TL::kChunkElems;
+      const int e = ((wave * TL::kChunksPerThread + u) * 64 + l) * TL::kChunkElems;
       *reinterpret_cast<u32x4*>(k_st[a] + e) = u32x4{0u, 0u, 0u, 0u};
       *reinterpret_cast<u32x4*>(v_st[a] + e) = u32x4{0u, 0u, 0u, 0u};
     }
