@@ -332,6 +332,31 @@ mvr::PagedAttentionPlan make_plan(const mvr_paged_attention_args* a, bool allow_
   // 34-52% at 512..8K tokens.  Unpadded was equal or better on every other
   // workload measured, the verify workload with its shared prefixes included.
   plan.num_units = base_units * (plan.block_merge ? plan.block_waves : plan.max_parts);
+  // Block shape of plans without block merge: 4 wavefronts (4 KV heads of one
+  // partition on one CU) or 1.  The dispatcher deals blocks to the 8 XCDs
+  // round-robin, so with 4-wavefront blocks and a multiple of 32 units per
+  // sequence, partition p of every sequence lands on the same two XCDs; in a
+  // ragged batch the early partitions, live in every sequence, then pile onto
+  // the same XCDs.  1-wavefront blocks with 8 KV heads put head h on XCD h:
+  // every XCD gets the same work, and a page shared by several sequences is
+  // read by one XCD per head slab.  Measured (HIP events, F16 D=128 unless
+  // noted), 4 -> 1 wavefronts: 16 x U[1K,8K] 66.5 -> 56.7 us, F32 143.6 ->
+  // 124.7, the 64-sequence shared-prompt batch 235.7 -> 224.4, dense plans
+  // 1-6% faster; where the 4-wavefront layout already rotates over the XCDs
+  // (16 x U[1K,16K], 8 x U[2K,32K], the verify batch) and on uniform batches
+  // 1-wavefront blocks were 1-4% slower.  Grids of fewer 4-wavefront blocks
+  // than CUs also take 1-wavefront blocks, which spread them over more CUs
+  // (one 512-token F32 sequence 13.1 -> 12.1 us).  MVR_ATTN_UNIT_WAVES=1, 2
+  // or 4 forces a shape.
+  plan.unit_waves = 4;
+  if (!plan.block_merge) {
+    const int64_t units_per_seq = (int64_t)a->num_kv_heads * plan.row_tiles * plan.max_parts;
+    if (plan.dense_parts || (ragged && units_per_seq % 32 == 0) || plan.num_units < 4LL * device_cus())
+      plan.unit_waves = 1;
+    static const int unit_waves_override = env_int("MVR_ATTN_UNIT_WAVES", 0);
+    if (unit_waves_override == 1 || unit_waves_override == 2 || unit_waves_override == 4)
+      plan.unit_waves = unit_waves_override;
+  }
   plan.partial_bytes = 0;
   if (plan.max_parts > 1 && !plan.block_merge) {
     // [partial o][partial m, l]

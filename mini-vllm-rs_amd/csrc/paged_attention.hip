@@ -373,7 +373,8 @@ struct F32Traits {
 // latency (16 sequences of 1.9K..14.8K tokens: 120 -> 106 us), and loses
 // where a third wavefront per SIMD had work (128 ragged sequences).
 // Block shape of a variant: WPB wavefronts; 16-wavefront blocks (4 per SIMD)
-// leave 128 VGPRs per lane.
+// leave 128 VGPRs per lane.  Blocks of 1, 2 or 4 wavefronts without block
+// merge compile to the same registers per wavefront.
 template <typename Tr, int NB, int DEPTH, int WPB>
 constexpr int kernel_min_blocks() {
   return WPB > kWavesPerBlock ? 1 : (DEPTH == 3 ? 2 : Tr::template min_blocks<NB>());
@@ -385,7 +386,8 @@ __global__ __launch_bounds__(kWaveSize* WPB, (kernel_min_blocks<Tr, NB, DEPTH, W
   typedef typename Tr::elem T;
   constexpr int kTileRows = 16 * NB;
   static_assert(DEPTH == 2 || (DEPTH == 3 && NB == 1 && D * sizeof(T) <= 256 && !BM), "unsupported pipeline depth");
-  static_assert(BM || WPB == kWavesPerBlock, "only block-merge plans change the block shape");
+  static_assert(BM ? (WPB == 4 || WPB == 8 || WPB == 16) : (WPB == 1 || WPB == 2 || WPB == 4),
+                "block shape: 4, 8 or 16 wavefronts with block merge, 1, 2 or 4 without");
   // Each wavefront's V tile, and (BM, after the key loop) each wavefront's
   // rows (O, m, l) in the same LDS: rows padded by 4 floats so that the 16
   // rows of a float4 store fall in distinct banks.
@@ -786,9 +788,31 @@ __global__ __launch_bounds__(256) void merge_partitions_kernel(PagedAttentionPar
   for (int e = 0; e < kPer; e++) dst[e] = (T)(acc[e] * inv);
 }
 
+// The split-context kernel without block merge, one unit per wavefront, in
+// blocks of WPB wavefronts (its wavefronts share nothing but the block).
+template <typename Tr, int D, int NB, int WPB>
+hipError_t launch_units(const PagedAttentionPlan& plan, const PagedAttentionParams& params, hipStream_t stream) {
+  const int64_t blocks = (plan.num_units + WPB - 1) / WPB;
+  if (plan.dense_parts) {
+    if (params.row_tiles != 1) return hipErrorInvalidValue; // dense_unit walks row tile 0 only
+    hipLaunchKernelGGL((paged_attention_kernel<Tr, D, NB, false, true, 2, WPB>), dim3((unsigned)blocks),
+                       dim3(kWaveSize * WPB), 0, stream, params);
+  } else if (plan.deep_pipeline) {
+    if constexpr (NB == 1 && D * sizeof(typename Tr::elem) <= 256) {
+      hipLaunchKernelGGL((paged_attention_kernel<Tr, D, NB, false, false, 3, WPB>), dim3((unsigned)blocks),
+                         dim3(kWaveSize * WPB), 0, stream, params);
+    } else {
+      return hipErrorInvalidValue; // planned only where the registers allow three chunks in flight
+    }
+  } else {
+    hipLaunchKernelGGL((paged_attention_kernel<Tr, D, NB, false, false, 2, WPB>), dim3((unsigned)blocks),
+                       dim3(kWaveSize * WPB), 0, stream, params);
+  }
+  return hipGetLastError();
+}
+
 template <typename Tr, int D, int NB>
 hipError_t launch_typed(const PagedAttentionPlan& plan, const PagedAttentionParams& params, hipStream_t stream) {
-  const int64_t blocks = (plan.num_units + kWavesPerBlock - 1) / kWavesPerBlock;
   if constexpr (NB == 1) {
     if (plan.block_merge) {
       // One block of block_waves wavefronts per (sequence, KV head, row tile).
@@ -815,22 +839,17 @@ hipError_t launch_typed(const PagedAttentionPlan& plan, const PagedAttentionPara
     }
   }
   if (plan.block_merge) return hipErrorInvalidValue; // planned for one 16-row block only
-  if (plan.dense_parts) {
-    if (params.row_tiles != 1) return hipErrorInvalidValue; // dense_unit walks row tile 0 only
-    hipLaunchKernelGGL((paged_attention_kernel<Tr, D, NB, false, true>), dim3((unsigned)blocks),
-                       dim3(kWaveSize * kWavesPerBlock), 0, stream, params);
-  } else if (plan.deep_pipeline) {
-    if constexpr (NB == 1 && D * sizeof(typename Tr::elem) <= 256) {
-      hipLaunchKernelGGL((paged_attention_kernel<Tr, D, NB, false, false, 3>), dim3((unsigned)blocks),
-                         dim3(kWaveSize * kWavesPerBlock), 0, stream, params);
-    } else {
-      return hipErrorInvalidValue; // planned only where the registers allow three chunks in flight
-    }
+  const int uw = plan.unit_waves == 0 ? kWavesPerBlock : plan.unit_waves;
+  hipError_t err;
+  if (uw == 1) {
+    err = launch_units<Tr, D, NB, 1>(plan, params, stream);
+  } else if (uw == 2) {
+    err = launch_units<Tr, D, NB, 2>(plan, params, stream);
+  } else if (uw == 4) {
+    err = launch_units<Tr, D, NB, 4>(plan, params, stream);
   } else {
-    hipLaunchKernelGGL((paged_attention_kernel<Tr, D, NB>), dim3((unsigned)blocks), dim3(kWaveSize * kWavesPerBlock),
-                       0, stream, params);
+    return hipErrorInvalidValue;
   }
-  hipError_t err = hipGetLastError();
   if (err != hipSuccess || plan.max_parts <= 1) return err;
   const int64_t tiles = (int64_t)params.num_seqs * params.num_kv_heads * params.row_tiles;
   hipLaunchKernelGGL((merge_partitions_kernel<typename Tr::elem, D, NB>), dim3((unsigned)(tiles * 4 * NB)),

@@ -72,6 +72,7 @@ struct PagedAttentionPlan {
   int block_waves;      // block_merge: wavefronts per block, 4, 8 or 16 (>= max_parts)
   bool dense_parts;     // ragged split plan: live units first, in a dense order (see dense_unit)
   bool deep_pipeline;   // three chunks in flight per wavefront instead of two (16-row tiles only)
+  int unit_waves;       // split plans without block merge: wavefronts per block, 1, 2 or 4 (0 means 4)
 };
 
 hipError_t launch_paged_attention(const PagedAttentionPlan& plan, PagedAttentionParams params, hipStream_t stream);
