@@ -302,8 +302,13 @@ mvr::PagedAttentionPlan make_plan(const mvr_paged_attention_args* a, bool allow_
     // alignment that more, shorter units would break.  Measured (F16 D=128
     // decode, U[L/8, L]): 128 x 8K 494 -> 440 us, 128 x 16K 1001 -> 901,
     // 32 x 4K 69 -> 65, 64 x 2K 73 -> 70; contexts up to 1K tokens (their
-    // 2-chunk floor) lost 5% (256 x 512), so they keep 80%.
-    int64_t u = ragged_units_per_group * 6 / 5;
+    // 2-chunk floor) lost 5% (256 x 512), so they keep 80%.  Key rows of more
+    // than 256 bytes (F32 at head_dim 128: twice the bytes per unit of F16)
+    // split for 180%: measured on F32 D=128, U[L/8, L] 32 x 4K 142 -> 136 us,
+    // 48 x 8K 373 -> 340, 64 x 2K 150 -> 139, 64 x 8K 509 -> 460, 128 x 8K
+    // 963 -> 937, 32 x 16K 500 -> 444; F16 and F32 D=64 lost 5-12% there.
+    const bool wide_rows = (int64_t)a->head_dim * (a->dtype == MVR_DTYPE_F16 ? 2 : 4) > 256;
+    int64_t u = ragged_units_per_group * (wide_rows ? 9 : 6) / 5;
     if (u < 1) u = 1;
     int64_t c = (ragged_total_chunks + u - 1) / u;
     if (c < ragged_floor) c = ragged_floor;

@@ -6,7 +6,8 @@ lets each wavefront find its unit with a wave-wide scan of the sequence
 lengths (dense_unit).  Same bar as every call: 2e-3 (F16) / 1e-5 (F32)
 against the oracle.  Covers 64 sequences of 257..2049 tokens (F16, D=128), 150
 sequences of 17..1024 tokens (more than one 64-sequence block of the scan, the
-F16 D=64 kernel) and 40 F32 sequences.  By default a dense plan also splits
+F16 D=64 kernel) and 40 F32 sequences at D=64 and at D=128 (whose key rows
+of 512 bytes take the finer dense split).  By default a dense plan also splits
 contexts into more partitions than the slot == partition plan of the same
 batch (a higher fill target), which changes the rounding.  With the same
 partitions the dense layout only changes which wavefront computes which
@@ -61,6 +62,7 @@ CASES = {
     "f16-d128-64x[257,2049]": ("f16", 32, 8, 128, 64, 257, 2049, 71),
     "f16-d64-150x[17,1024]": ("f16", 14, 2, 64, 150, 17, 1024, 72),
     "f32-d64-40x[100,3000]": ("f32", 14, 2, 64, 40, 100, 3000, 73),
+    "f32-d128-40x[512,4096]": ("f32", 32, 8, 128, 40, 512, 4096, 74),
 }
 
 
