@@ -111,7 +111,7 @@ _CHILD = (
 )
 
 
-FIXED_CHUNKS = {"f16-d128-64x[257,2049]": "8", "f16-d64-150x[17,1024]": "4"}
+FIXED_CHUNKS = {"f16-d128-64x[257,2049]": "8", "f16-d64-150x[17,1024]": "4", "f32-d128-40x[512,4096]": "8"}
 
 
 def _run_child(name, dst, **env):
