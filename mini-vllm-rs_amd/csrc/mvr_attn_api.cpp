@@ -349,14 +349,17 @@ mvr::PagedAttentionPlan make_plan(const mvr_paged_attention_args* a, bool allow_
   // 124.7, the 64-sequence shared-prompt batch 235.7 -> 224.4, dense plans
   // 1-6% faster; where the 4-wavefront layout already rotates over the XCDs
   // (16 x U[1K,16K], 8 x U[2K,32K], the verify batch) and on uniform batches
-  // 1-wavefront blocks were 1-4% slower.  Grids of fewer 4-wavefront blocks
-  // than CUs also take 1-wavefront blocks, which spread them over more CUs
-  // (one 512-token F32 sequence 13.1 -> 12.1 us).  MVR_ATTN_UNIT_WAVES=1, 2
-  // or 4 forces a shape.
+  // 1-wavefront blocks were 1-4% slower.  F32 units, twice the bytes of F16
+  // ones, take 1-wavefront blocks whatever the layout (24 x U[1K,8K] D=128
+  // 201 -> 171 us, 16 x U[2K,32K] 454 -> 408; one case of eight 3% slower).
+  // Grids of fewer 4-wavefront blocks than CUs also take 1-wavefront blocks,
+  // which spread them over more CUs (one 512-token F32 sequence 13.1 -> 12.1
+  // us).  MVR_ATTN_UNIT_WAVES=1, 2 or 4 forces a shape.
   plan.unit_waves = 4;
   if (!plan.block_merge) {
     const int64_t units_per_seq = (int64_t)a->num_kv_heads * plan.row_tiles * plan.max_parts;
-    if (plan.dense_parts || (ragged && units_per_seq % 32 == 0) || plan.num_units < 4LL * device_cus())
+    if (plan.dense_parts || a->dtype != MVR_DTYPE_F16 || (ragged && units_per_seq % 32 == 0) ||
+        plan.num_units < 4LL * device_cus())
       plan.unit_waves = 1;
     static const int unit_waves_override = env_int("MVR_ATTN_UNIT_WAVES", 0);
     if (unit_waves_override == 1 || unit_waves_override == 2 || unit_waves_override == 4)

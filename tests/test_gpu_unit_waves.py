@@ -2,8 +2,9 @@
 
 Plans without block merge run one unit (sequence, KV head, row tile,
 partition) per wavefront, in blocks of 4 wavefronts or of 1 (the planner's
-choice: 1 for dense plans, for ragged plans with a multiple of 32 units per
-sequence and for grids of fewer 4-wavefront blocks than CUs; 2 on request).
+choice: 1 for dense plans, for F32, for ragged plans with a multiple of 32
+units per sequence and for grids of fewer 4-wavefront blocks than CUs; 2 on
+request).
 The shape moves units between CUs and XCDs but changes nothing a unit
 computes, so every shape must give the same bits.  Cases, one per branch:
   * 16 F16 sequences of 1,024..8,192 tokens, 32/8 heads, D=128 (slot layout,
