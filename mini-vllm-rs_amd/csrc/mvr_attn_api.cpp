@@ -204,6 +204,8 @@ mvr::PagedAttentionPlan make_plan(const mvr_paged_attention_args* a, bool allow_
   const int64_t base_units = (int64_t)a->num_seqs * a->num_kv_heads * plan.row_tiles;
   const bool ragged = a->sum_seq_lens > 0 && a->sum_seq_lens < (int64_t)a->max_seq_len * a->num_seqs;
   int cpp = chunks_per_partition_override();
+  const bool cpp_override_none = cpp <= 0;
+  constexpr int kMaxPlannedParts = 128;
   // Kept for a dense ragged plan, which re-splits at a higher fill below.
   int64_t ragged_units_per_group = 0, ragged_total_chunks = 0, ragged_floor = 0;
   if (cpp <= 0) {
@@ -314,6 +316,17 @@ mvr::PagedAttentionPlan make_plan(const mvr_paged_attention_args* a, bool allow_
     if (c < ragged_floor) c = ragged_floor;
     if (c > max_chunks) c = max_chunks;
     plan.chunks_per_part = (int)c;
+    plan.max_parts = (max_chunks + plan.chunks_per_part - 1) / plan.chunks_per_part;
+  }
+  // At most 128 partitions per tile: the merge kernel reads a row's partials
+  // 32 per round trip, so a few long sequences over few KV heads split into
+  // hundreds of partitions (one 32K-token sequence over 2 KV heads: 513) pay
+  // more in the merge than the extra units save.  Measured (decode, one
+  // query per sequence): Qwen2-0.5B F16 1 x 32K 29.1 -> 20.4 us, F32 31.6 ->
+  // 29.5, 4 x 16K 23.4 -> 18.7; Llama-3-8B F16 1 x 32K 41.3 -> 34.6, F32
+  // 65.5 -> 57.3; caps of 64 lost up to 30% on the Qwen2-0.5B ones.
+  if (cpp_override_none && plan.max_parts > kMaxPlannedParts) {
+    plan.chunks_per_part = (max_chunks + kMaxPlannedParts - 1) / kMaxPlannedParts;
     plan.max_parts = (max_chunks + plan.chunks_per_part - 1) / plan.chunks_per_part;
   }
   // Deep pipeline (three chunks in flight per wavefront) for the ragged plans

@@ -708,6 +708,7 @@ __global__ __launch_bounds__(256) void merge_partitions_kernel(PagedAttentionPar
   constexpr int kBlocksPerTile = kTileRows / kWavesPerBlock;
   constexpr int kPer = D / kWaveSize; // output elements per lane
   constexpr int kInFlight = 8;
+  constexpr int kInFlightWide = 32;
   const int tile = blockIdx.x / kBlocksPerTile;
   const int lr = (blockIdx.x % kBlocksPerTile) * kWavesPerBlock + __builtin_amdgcn_readfirstlane(threadIdx.x / kWaveSize);
   const int l = lane_id();
@@ -744,6 +745,21 @@ __global__ __launch_bounds__(256) void merge_partitions_kernel(PagedAttentionPar
     const int cnt = min(kWaveSize, n_parts - j0);
     const float* base = p.partial_o + (prow0 + (int64_t)j0 * kTileRows) * D + l * kPer;
     int jj = 0;
+    // Rows with many partitions (a few long sequences over few KV heads split
+    // into hundreds) take 32 partial rows per round trip.
+    for (; jj + kInFlightWide <= cnt; jj += kInFlightWide) {
+      float v[kInFlightWide][kPer];
+#pragma unroll
+      for (int u = 0; u < kInFlightWide; u++)
+#pragma unroll
+        for (int e = 0; e < kPer; e++) v[u][e] = base[(int64_t)(jj + u) * kTileRows * D + e];
+#pragma unroll
+      for (int u = 0; u < kInFlightWide; u++) {
+        const float wu = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), jj + u));
+#pragma unroll
+        for (int e = 0; e < kPer; e++) acc[e] = fmaf(wu, v[u][e], acc[e]);
+      }
+    }
     for (; jj + kInFlight <= cnt; jj += kInFlight) {
       float v[kInFlight][kPer];
 #pragma unroll

@@ -329,6 +329,27 @@ def test_prefill_shapes_match_oracle(shape, dtype):
     assert np.isfinite(out).all() and err <= TOL[dtype], err
 
 
+@pytest.mark.parametrize("shape", [
+    # (hq, hkv, d, cached contexts): few long sequences over few KV heads, whose plans hit the cap of 128
+    # partitions per tile and whose merge reads 32 partials per round trip
+    (14, 2, 64, [32767]),
+    (14, 2, 64, [16383, 9000, 16383, 12000]),
+    (32, 8, 128, [32767]),
+])
+@pytest.mark.parametrize("dtype", ["f16", "f32"])
+def test_long_contexts_over_few_heads_match_oracle(shape, dtype):
+    hq, hkv, d, ctx = shape
+    w = _ragged_workload("long-context", 61 + len(ctx), hq, hkv, d, ctx, [1] * len(ctx), dtype=dtype)
+    say(f"[long] {dtype} {shape}")
+    vals = W.host_values(w)
+    t = W.device_tensors(w, vals)
+    out = run_hip(w, t).float().cpu().numpy()
+    ref = run_oracle(w, vals)
+    err = np.abs(out - ref).max()
+    say(f"[long] {dtype} {shape}: max-abs vs oracle {err:.3e}")
+    assert np.isfinite(out).all() and err <= TOL[dtype], err
+
+
 def test_reconstruct_contiguous_matches_reference_gather():
     """paged_cache.rs:363-391 on the device, bit for bit against the oracle's gather: the reference fixture
     (page size 3, table [2, 0], 5 tokens, head_dim 2, F32) and random F16/F32 pools with partial last pages."""
