@@ -697,7 +697,8 @@ __global__ __launch_bounds__(kWaveSize* WPB, (kernel_min_blocks<Tr, NB, DEPTH, W
 // One wavefront per (b, h, rt, row); a 256-thread block covers 4 rows of one
 // tile.  Lane j holds partition j's weight (64 partitions per round), the
 // partial rows are streamed as one coalesced 4*D-byte row per load with the
-// weight broadcast by readlane, eight rows in flight.  Rows and tiles that
+// weight broadcast by readlane, 32 rows in flight while at least 32 remain
+// and eight after that (always accumulated in partition order).  Rows and tiles that
 // were not split exit at once.
 // (A fused "last wavefront merges" variant with per-tile arrival counters
 // measured 43% slower on MI355X: each wavefront's device-scope release fence
