@@ -697,19 +697,22 @@ __global__ __launch_bounds__(kWaveSize* WPB, (kernel_min_blocks<Tr, NB, DEPTH, W
 // One wavefront per (b, h, rt, row); a 256-thread block covers 4 rows of one
 // tile.  Lane j holds partition j's weight (64 partitions per round), the
 // partial rows are streamed as one coalesced 4*D-byte row per load with the
-// weight broadcast by readlane, 32 rows in flight while at least 32 remain
-// and eight after that (always accumulated in partition order).  Rows and tiles that
+// weight broadcast by readlane, eight rows in flight, or (kWide, for plans of
+// more than 64 partitions per tile) 32 while at least 32 remain and eight
+// after that; always accumulated in partition order, so both give the same
+// bits.  The 32-row rounds cost registers: on 8,192 rows of ~32 partitions
+// (a cascade suffix pass) they took the merge from 7.9 to 10.1 us.  Rows and tiles that
 // were not split exit at once.
 // (A fused "last wavefront merges" variant with per-tile arrival counters
 // measured 43% slower on MI355X: each wavefront's device-scope release fence
 // writes back its XCD's L2, and those write-backs serialise.)
-template <typename T, int D, int NB>
+template <typename T, int D, int NB, bool kWide>
 __global__ __launch_bounds__(256) void merge_partitions_kernel(PagedAttentionParams p) {
   constexpr int kTileRows = 16 * NB;
   constexpr int kBlocksPerTile = kTileRows / kWavesPerBlock;
   constexpr int kPer = D / kWaveSize; // output elements per lane
   constexpr int kInFlight = 8;
-  constexpr int kInFlightWide = 32;
+  constexpr int kInFlightWide = kWide ? 32 : kInFlight;
   const int tile = blockIdx.x / kBlocksPerTile;
   const int lr = (blockIdx.x % kBlocksPerTile) * kWavesPerBlock + __builtin_amdgcn_readfirstlane(threadIdx.x / kWaveSize);
   const int l = lane_id();
@@ -748,7 +751,7 @@ __global__ __launch_bounds__(256) void merge_partitions_kernel(PagedAttentionPar
     int jj = 0;
     // Rows with many partitions (a few long sequences over few KV heads split
     // into hundreds) take 32 partial rows per round trip.
-    for (; jj + kInFlightWide <= cnt; jj += kInFlightWide) {
+    for (; kWide && jj + kInFlightWide <= cnt; jj += kInFlightWide) {
       float v[kInFlightWide][kPer];
 #pragma unroll
       for (int u = 0; u < kInFlightWide; u++)
@@ -869,8 +872,13 @@ hipError_t launch_typed(const PagedAttentionPlan& plan, const PagedAttentionPara
   }
   if (err != hipSuccess || plan.max_parts <= 1) return err;
   const int64_t tiles = (int64_t)params.num_seqs * params.num_kv_heads * params.row_tiles;
-  hipLaunchKernelGGL((merge_partitions_kernel<typename Tr::elem, D, NB>), dim3((unsigned)(tiles * 4 * NB)),
-                     dim3(kWaveSize * kWavesPerBlock), 0, stream, params);
+  if (plan.max_parts > 64) {
+    hipLaunchKernelGGL((merge_partitions_kernel<typename Tr::elem, D, NB, true>), dim3((unsigned)(tiles * 4 * NB)),
+                       dim3(kWaveSize * kWavesPerBlock), 0, stream, params);
+  } else {
+    hipLaunchKernelGGL((merge_partitions_kernel<typename Tr::elem, D, NB, false>), dim3((unsigned)(tiles * 4 * NB)),
+                       dim3(kWaveSize * kWavesPerBlock), 0, stream, params);
+  }
   return hipGetLastError();
 }
 
