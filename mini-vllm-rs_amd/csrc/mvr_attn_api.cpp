@@ -213,8 +213,21 @@ mvr::PagedAttentionPlan make_plan(const mvr_paged_attention_args* a, bool allow_
     // the device once: more partitions add merge traffic and a tail round,
     // fewer leave CUs idle.
     int64_t slots = target_waves_override();
-    if (slots <= 0) slots = mvr::paged_attention_resident_waves(plan.dtype, plan.head_dim, plan.row_blocks);
-    if (slots <= 0) slots = 256 * 8; // no device to ask (sizing only)
+    if (slots <= 0) {
+      slots = mvr::paged_attention_resident_waves(plan.dtype, plan.head_dim, plan.row_blocks);
+      if (slots <= 0) slots = 256 * 8; // no device to ask (sizing only)
+      // F16 at head_dim 64 keeps 2 KiB per page and KV head, half the bytes
+      // in flight per wavefront of head_dim 128, and its kernel fits four
+      // wavefronts per SIMD: calls reading at least 256 MiB of K/V plan for
+      // three per SIMD.  Measured (Qwen2-0.5B shape): uniform 64 x 16K (537
+      // MB) 125.8 -> 109.5 us, 128 x U[1K,8K] (295 MB) 66.6 -> 62.0, 64 x
+      // U[2K,16K] (295 MB) 65.6 -> 62.3; calls of 134 MB (64 x 4K, 16 x 16K)
+      // lost 3%, F32 at head_dim 64 and head_dim 128 lost 1-10%.
+      const int64_t tokens = a->sum_seq_lens > 0 ? a->sum_seq_lens : (int64_t)a->max_seq_len * a->num_seqs;
+      if (a->dtype == MVR_DTYPE_F16 && a->head_dim == 64 &&
+          tokens * a->num_kv_heads * a->head_dim * 2 * 2 >= (int64_t)256 << 20)
+        slots = slots * 3 / 2;
+    }
     int64_t units_per_group = slots / ((int64_t)a->num_kv_heads * plan.row_tiles);
     if (units_per_group < 1) units_per_group = 1;
     int64_t c;

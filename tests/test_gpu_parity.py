@@ -350,6 +350,22 @@ def test_long_contexts_over_few_heads_match_oracle(shape, dtype):
     assert np.isfinite(out).all() and err <= TOL[dtype], err
 
 
+def test_large_f16_head_dim_64_batch_matches_oracle():
+    """64 Qwen2-0.5B-shape sequences of 8,000..10,000 tokens in F16 (about 300 MB of K/V): the planner fills
+    three wavefronts per SIMD for such calls, a finer split than smaller ones get."""
+    rng = np.random.default_rng(71)
+    ctx = [int(x) for x in rng.integers(8000, 10000, size=64)]
+    w = _ragged_workload("large-d64", 71, 14, 2, 64, ctx, [1] * 64, dtype="f16")
+    assert int(w.seq_lens.sum()) * 2 * 64 * 2 * 2 >= 256 << 20
+    vals = W.host_values(w)
+    t = W.device_tensors(w, vals)
+    out = run_hip(w, t).float().cpu().numpy()
+    ref = run_oracle(w, vals)
+    err = np.abs(out - ref).max()
+    say(f"[large-d64] max-abs vs oracle {err:.3e}")
+    assert np.isfinite(out).all() and err <= TOL["f16"], err
+
+
 def test_reconstruct_contiguous_matches_reference_gather():
     """paged_cache.rs:363-391 on the device, bit for bit against the oracle's gather: the reference fixture
     (page size 3, table [2, 0], 5 tokens, head_dim 2, F32) and random F16/F32 pools with partial last pages."""
