@@ -11,8 +11,8 @@
 // rotated K and the V rows straight through the block table.
 //
 // One block row (blockIdx.x) per packed token: the block finds its request
-// by a binary search of cu_q_lens and its page by one block-table entry, all
-// scalar loads.  Each thread then handles one 8-element item of one row:
+// from cu_q_lens and its page by one block-table entry.  Each thread handles
+// one 8-element item of one row:
 // the query heads (rotated to q_out), the KV heads (rotated into the key
 // pool) and the KV heads again (copied into the value pool).  Items of a row
 // are adjacent lanes, so every row is read and written with coalesced 8- or
@@ -70,19 +70,15 @@ struct Arith<half_t> {
   __device__ static float get(half4 v, int e) { return (float)v[e]; }
 };
 
-// Rotates the 4 pairs of item j of one row (common.rs:355-358):
-//   Neox pairs (i, i + D/2), Interleaved pairs (2i, 2i + 1), i = 4j .. 4j + 3.
+// Rotates the 4 pairs of one item (common.rs:355-358): lo and hi hold the
+// item's elements at lo_off and hi_off of its row (Neox pairs (i, i + D/2),
+// Interleaved pairs (2i, 2i + 1), i = 4j .. 4j + 3); the results go back to
+// ylo and yhi in the same places.
 template <typename T, int ROPE>
-__device__ __forceinline__ void rotate_item(const T* src, T* dst, const T* cos_row, const T* sin_row, int j, int D) {
+__device__ __forceinline__ void rotate_item(const typename Arith<T>::vec& lo, const typename Arith<T>::vec& hi,
+                                            const typename Arith<T>::vec& c, const typename Arith<T>::vec& s,
+                                            typename Arith<T>::vec& ylo, typename Arith<T>::vec& yhi) {
   typedef Arith<T> A;
-  typedef typename A::vec V;
-  const int lo_off = ROPE == 0 ? 4 * j : 8 * j;
-  const int hi_off = ROPE == 0 ? D / 2 + 4 * j : 8 * j + 4;
-  const V lo = A::load(src + lo_off);
-  const V hi = A::load(src + hi_off);
-  const V c = A::load(cos_row + 4 * j);
-  const V s = A::load(sin_row + 4 * j);
-  V ylo, yhi;
 #pragma unroll
   for (int e = 0; e < 4; e++) {
     float a, b;
@@ -107,65 +103,89 @@ __device__ __forceinline__ void rotate_item(const T* src, T* dst, const T* cos_r
       yhi[2 * e - 3] = (T)yb;
     }
   }
-  A::store(dst + lo_off, ylo);
-  A::store(dst + hi_off, yhi);
 }
 
+// One item per thread: blockIdx.y * kThreads + threadIdx.x over the token's
+// (Hq + 2 Hkv) * D/8 items.  The item's source elements depend on the token
+// only, so they are loaded first and their latency overlaps the lookup of the
+// token's request, position and page, a chain of dependent loads: cu_q_lens
+// (one vector load and a ballot for up to 63 requests, a binary search
+// beyond), seq_lens, then the rotary rows and the block-table entry.
 template <typename T, int ROPE>
 __global__ __launch_bounds__(kThreads) void rope_append_kernel(RopeAppendParams p) {
   typedef Arith<T> A;
+  typedef typename A::vec V;
   const int n = blockIdx.x; // packed token
+  const int D = p.head_dim;
+  const int items_per_row = D / kItem;
+  const int items = (p.num_q_heads + 2 * p.num_kv_heads) * items_per_row;
+  const int it = blockIdx.y * kThreads + threadIdx.x;
+  const bool active = it < items;
+  const int row = active ? it / items_per_row : 0;
+  const int j = it - row * items_per_row;
+  const int kind = row < p.num_q_heads ? 0 : row < p.num_q_heads + p.num_kv_heads ? 1 : 2; // Q, K, V
+  const int h = kind == 0 ? row : kind == 1 ? row - p.num_q_heads : row - p.num_q_heads - p.num_kv_heads;
+  const int lo_off = kind == 2 ? kItem * j : ROPE == 0 ? 4 * j : 8 * j;
+  const int hi_off = kind == 2 ? kItem * j + 4 : ROPE == 0 ? D / 2 + 4 * j : 8 * j + 4;
+  const T* src = kind == 0 ? static_cast<const T*>(p.q) + h * p.q_stride_head + (int64_t)n * p.q_stride_token
+               : kind == 1 ? static_cast<const T*>(p.k) + h * p.k_stride_head + (int64_t)n * p.k_stride_token
+                           : static_cast<const T*>(p.v) + h * p.v_stride_head + (int64_t)n * p.v_stride_token;
+  V lo{}, hi{};
+  if (active) {
+    lo = A::load(src + lo_off);
+    hi = A::load(src + hi_off);
+  }
+
   int b = 0, q_start = 0, q_len = p.total_q;
   if (p.cu_q_lens) {
-    // Largest b with cu_q_lens[b] <= n; uniform per block, so scalar loads.
-    const const_i32* cu = (const const_i32*)p.cu_q_lens;
-    int lo = 0, hi = p.num_seqs - 1;
-    while (lo < hi) {
-      const int mid = (lo + hi + 1) >> 1;
-      if (cu[mid] <= n)
-        lo = mid;
-      else
-        hi = mid - 1;
+    // Largest b with cu_q_lens[b] <= n (uniform per block).
+    if (p.num_seqs < 64) {
+      const int l = threadIdx.x & 63;
+      const int cu_l = l <= p.num_seqs ? p.cu_q_lens[l] : INT32_MAX;
+      const uint64_t le = __ballot(cu_l <= n);
+      b = max(__builtin_amdgcn_readfirstlane(__popcll(le)) - 1, 0); // cu_q_lens[0] = 0 <= n: at least one
+      q_start = __builtin_amdgcn_readlane(cu_l, b);
+      q_len = __builtin_amdgcn_readlane(cu_l, b + 1) - q_start;
+    } else {
+      const const_i32* cu = (const const_i32*)p.cu_q_lens;
+      int lo_b = 0, hi_b = p.num_seqs - 1;
+      while (lo_b < hi_b) {
+        const int mid = (lo_b + hi_b + 1) >> 1;
+        if (cu[mid] <= n)
+          lo_b = mid;
+        else
+          hi_b = mid - 1;
+      }
+      b = lo_b;
+      q_start = cu[b];
+      q_len = cu[b + 1] - q_start;
     }
-    b = lo;
-    q_start = cu[b];
-    q_len = cu[b + 1] - q_start;
   }
   const int seq_len = p.seq_lens ? ((const const_i32*)p.seq_lens)[b] : p.single_seq_len;
   const int pos = seq_len - q_len + (n - q_start); // cached_kv_len + i (kv_cache/utils.rs:20-24)
   // Positions outside [0, max_seq_len) only come from tables that break the
   // contract (seq_len < q_len or > max_seq_len): write nothing rather than
   // leave the block-table row, the rotary tables or the pools.
-  if (pos < 0 || pos >= p.single_seq_len) return;
+  if (pos < 0 || pos >= p.single_seq_len || !active) return;
   const const_i32* bt = (const const_i32*)p.block_tables + (int64_t)b * p.block_table_stride;
   const int64_t page = bt[pos / p.page_size];
   const int slot = pos % p.page_size;
-
-  const int D = p.head_dim;
-  const int items_per_row = D / kItem;
-  const int items = (p.num_q_heads + 2 * p.num_kv_heads) * items_per_row;
+  T* dst = kind == 0 ? static_cast<T*>(p.q_out) + h * p.q_out_stride_head + (int64_t)n * p.q_out_stride_token
+         : kind == 1 ? static_cast<T*>(p.key_pool) + ((page * p.num_kv_heads + h) * p.page_size + slot) * D
+                     : static_cast<T*>(p.value_pool) + ((page * p.num_kv_heads + h) * p.page_size + slot) * D;
+  if (kind == 2) {
+    A::store(dst + lo_off, lo);
+    A::store(dst + hi_off, hi);
+    return;
+  }
   const T* cos_row = static_cast<const T*>(p.cos_table) + (int64_t)pos * (D / 2);
   const T* sin_row = static_cast<const T*>(p.sin_table) + (int64_t)pos * (D / 2);
-  for (int it = blockIdx.y * kThreads + threadIdx.x; it < items; it += gridDim.y * kThreads) {
-    const int row = it / items_per_row;
-    const int j = it - row * items_per_row;
-    if (row < p.num_q_heads) {
-      const T* src = static_cast<const T*>(p.q) + row * p.q_stride_head + (int64_t)n * p.q_stride_token;
-      T* dst = static_cast<T*>(p.q_out) + row * p.q_out_stride_head + (int64_t)n * p.q_out_stride_token;
-      rotate_item<T, ROPE>(src, dst, cos_row, sin_row, j, D);
-    } else if (row < p.num_q_heads + p.num_kv_heads) {
-      const int h = row - p.num_q_heads;
-      const T* src = static_cast<const T*>(p.k) + h * p.k_stride_head + (int64_t)n * p.k_stride_token;
-      T* dst = static_cast<T*>(p.key_pool) + ((page * p.num_kv_heads + h) * p.page_size + slot) * D;
-      rotate_item<T, ROPE>(src, dst, cos_row, sin_row, j, D);
-    } else {
-      const int h = row - p.num_q_heads - p.num_kv_heads;
-      const T* src = static_cast<const T*>(p.v) + h * p.v_stride_head + (int64_t)n * p.v_stride_token + kItem * j;
-      T* dst = static_cast<T*>(p.value_pool) + ((page * p.num_kv_heads + h) * p.page_size + slot) * D + kItem * j;
-      A::store(dst, A::load(src));
-      A::store(dst + 4, A::load(src + 4));
-    }
-  }
+  const V c = A::load(cos_row + 4 * j);
+  const V sn = A::load(sin_row + 4 * j);
+  V ylo, yhi;
+  rotate_item<T, ROPE>(lo, hi, c, sn, ylo, yhi);
+  A::store(dst + lo_off, ylo);
+  A::store(dst + hi_off, yhi);
 }
 
 template <typename T, int ROPE>
