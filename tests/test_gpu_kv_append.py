@@ -6,7 +6,8 @@ keys in their page slots and copied values equal the oracle's
 (oracle/kv_append_oracle.c) bit for bit, and every slot the append does not
 own keeps its previous contents.  Covers F16 and F32, Neox and Interleaved
 rotation, head_dim 64/128, page sizes 16 and 5, ragged batches crossing page
-boundaries, in-place and token-major layouts, the reference's paged-cache
+boundaries (5 requests, and 63/64/65 around the request lookup's wavefront
+boundary), in-place and token-major layouts, the reference's paged-cache
 unit tests (paged_cache.rs:560-1017) replayed through the kernel, the
 attention call that follows, and a full-size Llama-3-8B decode step.
 """
@@ -116,6 +117,23 @@ def test_ragged_batch_is_bit_exact(dtype, rope_type, d):
     assert_same(kp, kp_ref)
     assert_same(vp, vp_ref)
     assert not np.array_equal(bits(kp), bits(c["kp"]))  # something was written
+
+
+@pytest.mark.parametrize("n", [63, 64, 65])
+def test_request_lookup_at_the_wavefront_boundary(n):
+    """The kernel finds a token's request with one wavefront-wide ballot over cu_q_lens for up to 63
+    requests and by binary search beyond; batches of 63, 64 and 65 ragged requests (1..4 new tokens on
+    0..40 cached ones) take both paths and their boundary."""
+    say(f"[rope-append] {n} requests")
+    rng = np.random.default_rng(n)
+    cached = [int(x) for x in rng.integers(0, 41, size=n)]
+    q_lens = [int(x) for x in rng.integers(1, 5, size=n)]
+    c = make_case(90 + n, "f16", 8, 2, 64, 16, cached=cached, q_lens=q_lens, num_pages=256)
+    q_ref, kp_ref, vp_ref = run_oracle(c, M.ROPE_NEOX)
+    q_out, kp, vp = run_hip(c, M.ROPE_NEOX)
+    assert_same(q_out, q_ref)
+    assert_same(kp, kp_ref)
+    assert_same(vp, vp_ref)
 
 
 @pytest.mark.parametrize("dtype", ["f16", "f32"])
