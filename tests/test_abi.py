@@ -157,6 +157,35 @@ def test_block_merge_plan_needs_no_workspace():
     assert M.workspace_size(ragged) > 0
 
 
+def _partial_bytes(units, tile_rows, d):
+    """Workspace of a split plan: fp32 partial rows [units * tile_rows][d] and their (m, l), each 256-aligned."""
+    rows = units * tile_rows
+    up = lambda x: (x + 255) // 256 * 256
+    return up(rows * d * 4) + up(rows * 2 * 4)
+
+
+def _one_token_rows(num_seqs, hq, d, **kw):
+    return _args(num_seqs=num_seqs, num_q_heads=hq, head_dim=d, q_stride_head=num_seqs * d, q_stride_token=d,
+                 out_stride_head=num_seqs * d, out_stride_token=d, **kw)
+
+
+def test_long_context_plans_cap_partitions_at_128():
+    # One 32K-token sequence over Qwen2-0.5B's 2 KV heads: filling the 2,048 planned slots alone would split its
+    # 2,048 chunks down to the 4-chunk floor (512 partitions per KV head); the planner caps a tile at 128.
+    a = _one_token_rows(1, 14, 64, num_kv_heads=2, max_seq_len=32768, max_pages_per_seq=2048)
+    assert M.workspace_size(a) == _partial_bytes(2 * 128, 16, 64)
+
+
+def test_large_f16_head_dim_64_calls_plan_three_wavefronts_per_simd():
+    # 64 x 16K tokens of F16 K/V at head_dim 64 (537 MB) plan for 1.5x the 2,048 slots: 1,536 units per KV head,
+    # 24 partitions per sequence.  A 64 x 4K batch (134 MB, below 256 MiB) keeps the 2,048 slots: 16 partitions,
+    # which fit one 16-wavefront block and merge in LDS (no workspace); under the larger target they would not.
+    big = _one_token_rows(64, 14, 64, num_kv_heads=2, max_seq_len=16384, max_pages_per_seq=1024, num_pages=65536)
+    assert M.workspace_size(big) == _partial_bytes(64 * 2 * 24, 16, 64)
+    small = _one_token_rows(64, 14, 64, num_kv_heads=2, max_seq_len=4096, max_pages_per_seq=256, num_pages=16384)
+    assert M.workspace_size(small) == 0
+
+
 def test_validate_mirrors_reference_errors():
     a = _args()
     bt = [[i for i in range(64)], [64 + i for i in range(64)]]
