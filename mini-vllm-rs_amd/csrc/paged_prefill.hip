@@ -215,7 +215,11 @@ __global__ __launch_bounds__(kWaves * 64, 1) void paged_prefill_kernel(PrefillPa
   const int h = pair % p.num_kv_heads;
   const int b = pair / p.num_kv_heads;
   const int split = local % p.kv_splits;
-  const int rt = local / p.kv_splits;
+  // Row tiles in reverse: a tile's causal key range grows with its rows, so
+  // the last tiles of a pair carry the most work and are dispatched first
+  // (longest first: fresh prompts 5-6% faster, Llama-3-8B 1 x 2048 75.3 ->
+  // 70.7 us, Qwen2-7B 1 x 8192 667.7 -> 632.6; chunks on a long prefix level).
+  const int rt = p.row_tiles - 1 - local / p.kv_splits;
 
   const SeqRows s = load_rows(p, b);
   const int rows = p.group_size * s.q_len;

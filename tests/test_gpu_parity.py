@@ -312,6 +312,7 @@ def _ragged_workload(name, seed, hq, hkv, d, ctx, qlens, page_size=16, dtype="f1
     # The kernel's two wavefront groups take alternating 32-token key tiles and merge at the end:
     (28, 4, 128, [0, 31], [16, 33], 16),                # one key tile (the second group sees none), two tiles
     (7, 1, 64, [40], [100], 16),                        # head_dim 64 with an odd number of key tiles
+    (32, 8, 128, [0], [1024], 16),                      # a fresh 1,024-token prompt: 8 row tiles of triangular work
 ])
 @pytest.mark.parametrize("dtype", ["f16", "f32"])
 def test_prefill_shapes_match_oracle(shape, dtype):
