@@ -313,6 +313,8 @@ def _ragged_workload(name, seed, hq, hkv, d, ctx, qlens, page_size=16, dtype="f1
     (28, 4, 128, [0, 31], [16, 33], 16),                # one key tile (the second group sees none), two tiles
     (7, 1, 64, [40], [100], 16),                        # head_dim 64 with an odd number of key tiles
     (32, 8, 128, [0], [1024], 16),                      # a fresh 1,024-token prompt: 8 row tiles of triangular work
+    (28, 4, 128, [300, 0, 1000], [256, 128, 384], 16),  # chunks of 1-3 position tiles: tiles ordered by position
+    (8, 2, 64, [0, 0], [512, 128], 32),                 # fresh prompts of unequal length, head_dim 64
 ])
 @pytest.mark.parametrize("dtype", ["f16", "f32"])
 def test_prefill_shapes_match_oracle(shape, dtype):
