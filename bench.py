@@ -404,6 +404,13 @@ def main():
             "3": measure(W, M, torch, lambda: W.llama3_8b_decode_b64_8k_f16(64, "f32"), max(20, a.steps // 2), a.warmup),
             "4": measure(W, M, torch, lambda: W.qwen2_7b_chunked_prefill_f16("f32"), max(20, a.steps // 2), a.warmup),
         }
+        log("[bench] fresh prompts (prefill with nothing cached)")
+        result["fresh_prompt"] = {
+            "llama3-8b 1x2048": measure(W, M, torch, lambda: W.fresh_prompt_f16("llama3-8b", 2048),
+                                        max(20, a.steps // 2), a.warmup),
+            "qwen2-7b 1x8192": measure(W, M, torch, lambda: W.fresh_prompt_f16("qwen2-7b", 8192),
+                                       max(20, a.steps // 2), a.warmup),
+        }
         log("[bench] mixed decode + prefill batch")
         result["mixed"] = measure_mixed(W, M, torch, max(20, a.steps // 2), a.warmup)
         log("[bench] config 5 through cascade attention")

@@ -159,6 +159,20 @@ def qwen2_7b_chunked_prefill_f16(dtype: str = "f16") -> Workload:
                     np.full(4, 256, np.int32), bt, seed)
 
 
+def fresh_prompt_f16(model: str = "llama3-8b", prompt: int = 2048, num_seqs: int = 1) -> Workload:
+    """Prefill of whole prompts with nothing cached (q_len = seq_len, the first chunk of a request when the
+    scheduler's budget admits the prompt at once): causal self-attention over the prompt, pages in random order.
+    model: "llama3-8b" (32 Q / 8 KV, D 128) or "qwen2-7b" (28 Q / 4 KV, D 128)."""
+    hq, hkv = {"llama3-8b": (32, 8), "qwen2-7b": (28, 4)}[model]
+    seed = SEED_BASE + 8
+    rng = np.random.default_rng(seed)
+    seq_lens = np.full(num_seqs, prompt, np.int32)
+    num_pages = num_seqs * math.ceil(prompt / 16)
+    bt = _assign_pages(rng, seq_lens, 16, num_pages)
+    return Workload(f"{model} fresh prompt f16 b{num_seqs} {prompt}", "f16", hq, hkv, 128, 16, num_pages, 0.3,
+                    seq_lens, np.full(num_seqs, prompt, np.int32), bt, seed)
+
+
 def llama3_8b_mixed_decode_prefill_f16(num_decode: int = 63, decode_ctx: int = 8192, prefix: int = 2048,
                                        chunk: int = 256, dtype: str = "f16") -> Workload:
     """The batch one scheduler step emits (scheduler.rs:258-271): the decode requests first, one token each,
