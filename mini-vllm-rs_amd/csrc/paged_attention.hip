@@ -35,6 +35,7 @@ typedef half_t half8 __attribute__((ext_vector_type(8)));
 typedef half_t half4 __attribute__((ext_vector_type(4)));
 typedef short short4v __attribute__((ext_vector_type(4)));
 typedef float float4v __attribute__((ext_vector_type(4)));
+typedef float float2v __attribute__((ext_vector_type(2)));
 
 typedef __attribute__((address_space(3))) short4v lds_short4;
 typedef __attribute__((address_space(4))) int32_t const_i32;
@@ -719,6 +720,14 @@ __global__ __launch_bounds__(256) void merge_partitions_kernel(PagedAttentionPar
   const int rt = tile % p.row_tiles;
   const int h = (tile / p.row_tiles) % p.num_kv_heads;
   const int b = tile / (p.row_tiles * p.num_kv_heads);
+  // Partial row of partition j: (tile * max_parts + j) * kTileRows + lr.  The
+  // workspace holds max_parts such slots for every tile, so lane j's (m, l)
+  // is requested beside the sequence's lengths instead of after them (one
+  // round trip less on small calls); slots past the tile's partition count
+  // hold nothing of this call and are dropped once that count is known.
+  const int64_t prow0 = (int64_t)tile * p.max_parts * kTileRows + lr;
+  float2v ml0 = {-INFINITY, 0.f};
+  if (l < p.max_parts) ml0 = *reinterpret_cast<const float2v*>(p.partial_ml + (prow0 + (int64_t)l * kTileRows) * 2);
   const SeqInfo s = load_seq(p, b);
   const int rho = rt * kTileRows + lr;
   if (rho >= p.group_size * s.q_len) return;
@@ -727,10 +736,26 @@ __global__ __launch_bounds__(256) void merge_partitions_kernel(PagedAttentionPar
   const int n_parts = min(tile_parts(s, n_chunks, p.chunks_per_part), p.max_parts);
   if (n_parts <= 1) return;
 
-  // Partial row of partition j: (tile * max_parts + j) * kTileRows + lr.
-  const int64_t prow0 = (int64_t)tile * p.max_parts * kTileRows + lr;
-  float mmax = -INFINITY;
-  for (int j = l; j < n_parts; j += kWaveSize) mmax = fmaxf(mmax, p.partial_ml[(prow0 + (int64_t)j * kTileRows) * 2]);
+  // The first kFirst partial rows need only the partition count: they are in
+  // flight while the weights are reduced.  Not in the kWide variant, whose
+  // 32-row rounds already keep enough in flight (there the extra registers
+  // measured 2% slower on single 32K-token contexts).
+  constexpr int kFirst = kWide ? 0 : 32 / kPer;
+  const float* const base0 = p.partial_o + prow0 * D + l * kPer;
+  float v0[kFirst > 0 ? kFirst : 1][kPer];
+#pragma unroll
+  for (int u = 0; u < kFirst; u++) {
+#pragma unroll
+    for (int e = 0; e < kPer; e++) v0[u][e] = 0.f;
+    if (u < n_parts) {
+#pragma unroll
+      for (int e = 0; e < kPer; e++) v0[u][e] = base0[(int64_t)u * kTileRows * D + e];
+    }
+  }
+
+  float mmax = l < n_parts ? ml0[0] : -INFINITY;
+  for (int j = l + kWaveSize; j < n_parts; j += kWaveSize)
+    mmax = fmaxf(mmax, p.partial_ml[(prow0 + (int64_t)j * kTileRows) * 2]);
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) mmax = fmaxf(mmax, __shfl_xor(mmax, off));
   const float m_use = mmax == -INFINITY ? 0.f : mmax;
@@ -743,12 +768,24 @@ __global__ __launch_bounds__(256) void merge_partitions_kernel(PagedAttentionPar
     float w = 0.f;
     if (j0 + l < n_parts) {
       const int64_t prow = prow0 + (int64_t)(j0 + l) * kTileRows;
-      w = __builtin_amdgcn_exp2f(p.partial_ml[prow * 2] - m_use); // m = -inf (no visible key) gives 0
-      den += w * p.partial_ml[prow * 2 + 1];
+      const float2v ml = j0 == 0 ? ml0 : *reinterpret_cast<const float2v*>(p.partial_ml + prow * 2);
+      w = __builtin_amdgcn_exp2f(ml[0] - m_use); // m = -inf (no visible key) gives 0
+      den += w * ml[1];
     }
     const int cnt = min(kWaveSize, n_parts - j0);
     const float* base = p.partial_o + (prow0 + (int64_t)j0 * kTileRows) * D + l * kPer;
     int jj = 0;
+    if (kFirst > 0 && j0 == 0) {
+      jj = min(cnt, kFirst);
+#pragma unroll
+      for (int u = 0; u < kFirst; u++) {
+        if (u < jj) {
+          const float wu = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), u));
+#pragma unroll
+          for (int e = 0; e < kPer; e++) acc[e] = fmaf(wu, v0[u][e], acc[e]);
+        }
+      }
+    }
     // Rows with many partitions (a few long sequences over few KV heads split
     // into hundreds) take 32 partial rows per round trip.
     for (; kWide && jj + kInFlightWide <= cnt; jj += kInFlightWide) {
