@@ -263,7 +263,9 @@ def measure_mixed(W, M, torch, steps, warmup):
     the lengths), its two parts timed alone on the same tensors, and the two parts issued as separate calls
     back to back inside one timed step (parts_back_to_back: the same kernels in the same order as the routed
     call, so that the decode kernel follows a prefill as it does there; a decode kernel that follows
-    decodes only runs about 9 us faster)."""
+    decodes only runs about 9 us faster).  The routed call and the parts back to back are timed in
+    alternation, three rounds each, and the no-hints call (about a millisecond of prefill kernel per step)
+    last, so that no case runs right after a heavier one that the other does not follow."""
     w = W.llama3_8b_mixed_decode_prefill_f16()
     t = W.device_tensors(w, None)
     n_dec = int((w.q_lens == 1).sum())
@@ -276,12 +278,16 @@ def measure_mixed(W, M, torch, steps, warmup):
             dec.step()
             pre.step()
 
-    for key, r in (("no_hints", Runner(w, t, torch, M)), ("host_hints", Runner(w, t, torch, M, host_hints=True)),
-                   ("decodes_alone", dec), ("prefill_alone", pre), ("parts_back_to_back", BackToBack())):
-        _, per = time_steps(r, torch, steps, warmup)
+    runners = dict(decodes_alone=dec, prefill_alone=pre, host_hints=Runner(w, t, torch, M, host_hints=True),
+                   parts_back_to_back=BackToBack(), no_hints=Runner(w, t, torch, M))
+    samples = {key: [] for key in runners}
+    for key in ["decodes_alone", "prefill_alone"] + ["host_hints", "parts_back_to_back"] * 3 + ["no_hints"]:
+        _, per = time_steps(runners[key], torch, steps, warmup)
+        samples[key] += per
+    for key, per in samples.items():
+        per.sort()
         res[key + "_us"] = round(per[len(per) // 2], 2)
-        del r
-    del dec, pre
+    del runners, dec, pre
     res["sum_of_parts_us"] = round(res["decodes_alone_us"] + res["prefill_alone_us"], 2)
     res["host_hints_gbs"] = round(w.algorithmic_bytes() / (res["host_hints_us"] * 1e-6) / 1e9, 1)
     res["hbm_frac"] = round(res["host_hints_gbs"] / HBM_PEAK_GBS, 4)
