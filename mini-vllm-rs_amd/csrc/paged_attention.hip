@@ -740,16 +740,21 @@ __global__ __launch_bounds__(256) void merge_partitions_kernel(PagedAttentionPar
   // flight while the weights are reduced.  Not in the kWide variant, whose
   // 32-row rounds already keep enough in flight (there the extra registers
   // measured 2% slower on single 32K-token contexts).
-  constexpr int kFirst = kWide ? 0 : 32 / kPer;
+  // In groups of 8 rows (one uniform branch per group): a group's rows past
+  // the count read the last partial row again (in the tile, an L2 hit) and
+  // are left out of the sum below.
+  constexpr int kFirst = kWide ? 0 : 64 / kPer;
   const float* const base0 = p.partial_o + prow0 * D + l * kPer;
   float v0[kFirst > 0 ? kFirst : 1][kPer];
 #pragma unroll
-  for (int u = 0; u < kFirst; u++) {
+  for (int g8 = 0; g8 < kFirst; g8 += 8) {
+    if (g8 < n_parts) {
 #pragma unroll
-    for (int e = 0; e < kPer; e++) v0[u][e] = 0.f;
-    if (u < n_parts) {
+      for (int u = g8; u < g8 + 8; u++) {
+        const int64_t ju = min(u, n_parts - 1);
 #pragma unroll
-      for (int e = 0; e < kPer; e++) v0[u][e] = base0[(int64_t)u * kTileRows * D + e];
+        for (int e = 0; e < kPer; e++) v0[u][e] = base0[ju * kTileRows * D + e];
+      }
     }
   }
 
@@ -778,11 +783,14 @@ __global__ __launch_bounds__(256) void merge_partitions_kernel(PagedAttentionPar
     if (kFirst > 0 && j0 == 0) {
       jj = min(cnt, kFirst);
 #pragma unroll
-      for (int u = 0; u < kFirst; u++) {
-        if (u < jj) {
-          const float wu = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), u));
+      for (int g8 = 0; g8 < kFirst; g8 += 8) {
+        if (g8 < jj) {
 #pragma unroll
-          for (int e = 0; e < kPer; e++) acc[e] = fmaf(wu, v0[u][e], acc[e]);
+          for (int u = g8; u < g8 + 8; u++) {
+            const float wu = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w), u));
+#pragma unroll
+            for (int e = 0; e < kPer; e++) acc[e] = u < jj ? fmaf(wu, v0[u][e], acc[e]) : acc[e];
+          }
         }
       }
     }
