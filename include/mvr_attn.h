@@ -105,11 +105,14 @@ typedef struct mvr_paged_attention_args {
   int64_t sum_seq_lens;      /* optional planning hint: sum of seq_lens (0 = unknown, assume max_seq_len each) */
   /* Optional planning hints (NULL = unknown): host copies of seq_lens [num_seqs] and cu_q_lens [num_seqs + 1]
      holding the same values as the device tables (the caller builds them on the host before uploading; the
-     kernels read only the device tables).  With cu_q_lens_host, a batch that mixes decode-sized requests
-     (q_len * num_q_heads / num_kv_heads <= 32) with prefill-sized ones, as one scheduler step packs them
-     (scheduler.rs:258-271), runs each class as its own launch planned for it, instead of planning the whole
-     call for its longest query; seq_lens_host also sizes each class's context split exactly.  Read during
-     the call only. */
+     kernels read only the device tables).  A batch whose longest query is prefill-sized runs as two launches
+     over all of its sequences, one per class of request (decode-sized: q_len * num_q_heads / num_kv_heads
+     <= 32; prefill-sized), each planned for its class, as one scheduler step packs them
+     (scheduler.rs:258-271).  With cu_q_lens_host the planner knows the classes (one launch when there is one
+     class) and seq_lens_host sizes each class's context split.  Hints only shape the plans: every row is
+     computed from the device tables whatever they say, so a stale hint costs speed, not results (with
+     MVR_ATTN_CHECKED=true a hint that differs from the device tables is an error).  Read during the call
+     only. */
   const int32_t* seq_lens_host;
   const int32_t* cu_q_lens_host;
 } mvr_paged_attention_args;
@@ -146,7 +149,10 @@ int mvr_paged_attention(const mvr_paged_attention_args* args);
    calls that overlap in time on one device (other threads or streams) race,
    calls on one stream are ordered.  The array needs no initialisation:
    results never depend on what an earlier call left in it.  MVR_ATTN_CHECKED
-   does not apply to it. */
+   does not apply to it.  The first call on a device looks up the array's
+   device address (hipGetSymbolAddress, which may load the library's code
+   object): make one call on each device outside any stream capture before
+   capturing calls into a graph. */
 #define MVR_NOALLOC_SCRATCH_BYTES (64u << 20)
 int mvr_paged_attention_noalloc(const mvr_paged_attention_args* args);
 

@@ -164,8 +164,22 @@ int device_cus() {
   return cus;
 }
 
-mvr::PagedAttentionPlan make_plan(const mvr_paged_attention_args* a, bool allow_prefill = true) {
+// What a launch's sequences hold, for sizing only: a class launch of a mixed
+// batch spans every sequence of the call (its grid), but only the sequences of
+// its class have rows there.  Defaults: every sequence, at the call's bounds.
+struct LiveSeqs {
+  int64_t count = 0;   // sequences with rows in this launch (0: num_seqs)
+  int max_seq_len = 0; // their longest context (0: the call's max_seq_len)
+  int64_t split_count = 0; // prefill kernel: sequences given key splits and partial slots (0: num_seqs)
+};
+
+mvr::PagedAttentionPlan make_plan(const mvr_paged_attention_args* a, bool allow_prefill = true,
+                                  LiveSeqs live = LiveSeqs{}, bool force_prefill = false) {
   mvr::PagedAttentionPlan plan{};
+  // Sizing inputs (the grid itself always covers num_seqs sequences and the
+  // call's max_seq_len, which the kernels clamp device lengths to).
+  const int64_t n_live = live.count > 0 && live.count < a->num_seqs ? live.count : a->num_seqs;
+  const int len_live = live.max_seq_len > 0 && live.max_seq_len < a->max_seq_len ? live.max_seq_len : a->max_seq_len;
   plan.dtype = a->dtype;
   plan.head_dim = a->head_dim;
   const int group = a->num_q_heads / a->num_kv_heads;
@@ -175,24 +189,26 @@ mvr::PagedAttentionPlan make_plan(const mvr_paged_attention_args* a, bool allow_
   // MVR_ATTN_PREFILL_KERNEL=false keeps every call on the split-context kernel.
   static const bool prefill_enabled = env_bool("MVR_ATTN_PREFILL_KERNEL", true);
   const bool page_pow2 = (a->page_size & (a->page_size - 1)) == 0;
-  if (allow_prefill && prefill_enabled && rows_max > 64 && page_pow2) {
+  if (allow_prefill && prefill_enabled && (rows_max > 64 || force_prefill) && page_pow2) {
     plan.prefill = true;
     plan.row_tiles = (int)((rows_max + mvr::kPrefillBlockRows - 1) / mvr::kPrefillBlockRows);
     const int64_t base_blocks = (int64_t)a->num_seqs * a->num_kv_heads * plan.row_tiles;
-    const int key_tiles = (a->max_seq_len + 31) / 32;
+    const int64_t live_blocks = n_live * a->num_kv_heads * plan.row_tiles;
+    const int key_tiles = (len_live + 31) / 32;
     static const int split_override = env_int("MVR_ATTN_PREFILL_SPLITS", 0);
     int64_t splits = split_override;
     if (splits <= 0) {
       // Split keys only while blocks leave CUs idle: one 4-wavefront block
       // per CU ran faster than two half-length blocks plus the merge pass.
-      splits = (int64_t)device_cus() / base_blocks;
+      splits = (int64_t)device_cus() / live_blocks;
       if (splits > key_tiles / 8) splits = key_tiles / 8; // keep >= 8 key tiles per split
     }
     if (splits > 8) splits = 8; // the merge holds one split per lane; 8 is plenty
     if (splits < 1) splits = 1;
     plan.kv_splits = (int)splits;
     if (splits > 1) {
-      const size_t prow = (size_t)base_blocks * splits * mvr::kPrefillBlockRows;
+      const int64_t split_seqs = live.split_count > 0 && live.split_count < a->num_seqs ? live.split_count : a->num_seqs;
+      const size_t prow = (size_t)(split_seqs * a->num_kv_heads * plan.row_tiles) * splits * mvr::kPrefillBlockRows;
       plan.partial_bytes = align_up(prow * a->head_dim * sizeof(float), 256) + align_up(prow * 2 * sizeof(float), 256);
     }
     return plan;
@@ -200,9 +216,10 @@ mvr::PagedAttentionPlan make_plan(const mvr_paged_attention_args* a, bool allow_
   plan.row_blocks = rows_max <= 16 ? 1 : 2;
   const int tile_rows = 16 * plan.row_blocks;
   plan.row_tiles = (int)((rows_max + tile_rows - 1) / tile_rows);
-  const int max_chunks = (a->max_seq_len + mvr::kChunkTokens - 1) / mvr::kChunkTokens;
+  const int max_chunks = (a->max_seq_len + mvr::kChunkTokens - 1) / mvr::kChunkTokens; // the grid covers these
+  const int live_chunks = (len_live + mvr::kChunkTokens - 1) / mvr::kChunkTokens;      // and sizes for these
   const int64_t base_units = (int64_t)a->num_seqs * a->num_kv_heads * plan.row_tiles;
-  const bool ragged = a->sum_seq_lens > 0 && a->sum_seq_lens < (int64_t)a->max_seq_len * a->num_seqs;
+  const bool ragged = a->sum_seq_lens > 0 && a->sum_seq_lens < (int64_t)len_live * n_live;
   int cpp = chunks_per_partition_override();
   const bool cpp_override_none = cpp <= 0;
   constexpr int kMaxPlannedParts = 128;
@@ -223,7 +240,7 @@ mvr::PagedAttentionPlan make_plan(const mvr_paged_attention_args* a, bool allow_
       // MB) 125.8 -> 109.5 us, 128 x U[1K,8K] (295 MB) 66.6 -> 62.0, 64 x
       // U[2K,16K] (295 MB) 65.6 -> 62.3; calls of 134 MB (64 x 4K, 16 x 16K)
       // lost 3%, F32 at head_dim 64 and head_dim 128 lost 1-10%.
-      const int64_t tokens = a->sum_seq_lens > 0 ? a->sum_seq_lens : (int64_t)a->max_seq_len * a->num_seqs;
+      const int64_t tokens = a->sum_seq_lens > 0 ? a->sum_seq_lens : (int64_t)len_live * n_live;
       if (a->dtype == MVR_DTYPE_F16 && a->head_dim == 64 &&
           tokens * a->num_kv_heads * a->head_dim * 2 * 2 >= (int64_t)256 << 20)
         slots = slots * 3 / 2;
@@ -238,25 +255,25 @@ mvr::PagedAttentionPlan make_plan(const mvr_paged_attention_args* a, bool allow_
       // late ones'.  Plan for 80% of the slots to absorb both: on 16
       // sequences of 1K..16K tokens, 78% fill ran in 108 us and 95% in 132 us.
       const int64_t total_chunks =
-          (a->sum_seq_lens + mvr::kChunkTokens - 1) / mvr::kChunkTokens + a->num_seqs / 2;
+          (a->sum_seq_lens + mvr::kChunkTokens - 1) / mvr::kChunkTokens + n_live / 2;
       int64_t u = units_per_group * 4 / 5;
       if (u < 1) u = 1;
       c = (total_chunks + u - 1) / u;
     } else {
       // Every sequence planned at max_seq_len: num_seqs * ceil(max_chunks / c) units.
-      int64_t parts = units_per_group / a->num_seqs;
+      int64_t parts = units_per_group / n_live;
       if (parts < 1) parts = 1;
-      c = (max_chunks + parts - 1) / parts;
+      c = (live_chunks + parts - 1) / parts;
     }
     // Floor: small batches are bound by each wavefront's serial chain of
     // chunk loads, so they split down to 4 chunks per wavefront (2 for
     // contexts up to 1024 tokens); measured 17.9 -> 12.1 us on one 512-token
     // F32 sequence and 24 -> 14 us on 8 sequences of 128..4096 tokens.
-    const int64_t floor_cpp = max_chunks <= 64 ? 2 : 4;
+    const int64_t floor_cpp = live_chunks <= 64 ? 2 : 4;
     cpp = (int)(c < floor_cpp ? floor_cpp : (c > max_chunks ? max_chunks : c));
     if (ragged) {
       ragged_units_per_group = units_per_group;
-      ragged_total_chunks = (a->sum_seq_lens + mvr::kChunkTokens - 1) / mvr::kChunkTokens + a->num_seqs / 2;
+      ragged_total_chunks = (a->sum_seq_lens + mvr::kChunkTokens - 1) / mvr::kChunkTokens + n_live / 2;
       ragged_floor = floor_cpp;
     }
   }
@@ -304,13 +321,13 @@ mvr::PagedAttentionPlan make_plan(const mvr_paged_attention_args* a, bool allow_
   // turns it off.
   static const bool dense_enabled = env_bool("MVR_ATTN_DENSE_RAGGED", true);
   bool dense = false;
-  if (dense_enabled && ragged && plan.row_tiles == 1 && plan.max_parts > 1 && !plan.block_merge && a->num_seqs >= 32) {
+  if (dense_enabled && ragged && plan.row_tiles == 1 && plan.max_parts > 1 && !plan.block_merge && n_live >= 32) {
     const int64_t chunk_tokens = (int64_t)mvr::kChunkTokens * plan.chunks_per_part;
-    const int64_t est_live = (a->sum_seq_lens + chunk_tokens - 1) / chunk_tokens + a->num_seqs / 2;
+    const int64_t est_live = (a->sum_seq_lens + chunk_tokens - 1) / chunk_tokens + n_live / 2;
     dense = est_live * 10 < (int64_t)a->num_seqs * plan.max_parts * 7; // live fraction < 0.7
   }
   plan.dense_parts = dense;
-  if (dense && ragged_units_per_group > 0 && max_chunks > 64) {
+  if (dense && ragged_units_per_group > 0 && live_chunks > 64) {
     // Dense plans split for 120% of the resident slots instead of 80%:
     // in-order dispatch hands the extra units to whichever CU frees first,
     // and the layout has already given up the cross-sequence partition
@@ -407,7 +424,11 @@ namespace {
 // The extra inputs of one launch: the passes of cascade attention, and the
 // q_len class of one launch of a mixed batch (all null / 0 for a plain call).
 struct LaunchExtras {
-  int32_t class_q_min = 0, class_q_max = 0; // sequences outside [min, max] (max 0: unbounded) are skipped
+  int32_t class_q_min = 0, class_q_max = 0; // split-context kernel: sequences outside [min, max] (max 0: unbounded) are skipped
+  // Prefill kernel: sequences in [skip_seq_lo, skip_seq_hi] with q_len <= skip_q_max (0: none) are skipped;
+  // key splits only for [split_seq_lo, split_seq_lo + split_seq_count) (count 0: all).
+  int32_t skip_seq_lo = 0, skip_seq_hi = -1, skip_q_max = 0;
+  int32_t split_seq_lo = 0, split_seq_count = 0;
   const int32_t* key_begin = nullptr; // suffix pass: first key of each sequence
   const int32_t* key_end = nullptr;   // prefix pass: keys [0, key_end) of each group
   float* state_o = nullptr;           // normalised fp32 rows instead of `out`
@@ -442,8 +463,8 @@ int launch_planned(const mvr_paged_attention_args* a, const mvr::PagedAttentionP
     f.out_stride_head = a->out_stride_head;
     f.out_stride_token = a->out_stride_token;
     if (plan.partial_bytes) {
-      const size_t prow = (size_t)a->num_seqs * a->num_kv_heads * plan.row_tiles * plan.kv_splits *
-                          mvr::kPrefillBlockRows;
+      const size_t prow = (size_t)(cp.split_seq_count ? cp.split_seq_count : a->num_seqs) * a->num_kv_heads *
+                          plan.row_tiles * plan.kv_splits * mvr::kPrefillBlockRows;
       char* w = static_cast<char*>(ws);
       f.partial_o = reinterpret_cast<float*>(w);
       f.partial_ml = reinterpret_cast<float*>(w + align_up(prow * a->head_dim * sizeof(float), 256));
@@ -461,8 +482,13 @@ int launch_planned(const mvr_paged_attention_args* a, const mvr::PagedAttentionP
     f.state_o = cp.state_o;
     f.state_lse = cp.state_lse;
     f.state_tokens = cp.state_tokens;
-    f.class_q_min = cp.class_q_min;
-    f.class_q_max = cp.class_q_max;
+    if (cp.class_q_min > 0 || cp.class_q_max > 0)
+      return fail(MVR_E_INVALID_ARGUMENT, "internal: q_len class filter planned on the prefill kernel");
+    f.skip_seq_lo = cp.skip_seq_lo;
+    f.skip_seq_hi = cp.skip_seq_hi;
+    f.skip_q_max = cp.skip_q_max;
+    f.split_seq_lo = cp.split_seq_lo;
+    f.split_seq_count = cp.split_seq_count;
     TraceRange launch("attn-prefill-fused");
     hipError_t err = mvr::launch_paged_prefill(f, a->head_dim, a->dtype == MVR_DTYPE_F32, static_cast<hipStream_t>(a->stream));
     if (err != hipSuccess) return fail(MVR_E_HIP, "kernel launch failed: %s", hipGetErrorString(err));
@@ -521,15 +547,24 @@ int check_workspace(const mvr_paged_attention_args* a, size_t need) {
 }
 
 // One mvr_paged_attention call as one launch sequence, or two for a batch
-// that mixes decode-sized requests (grouped rows G * q_len <= kSmallRows: one
-// row tile of the split-context kernel) with prefill-sized ones.  Planned for
-// its longest query, such a call would give every decode sequence the prefill
-// kernel's 128-row tiles (or, in F32, 32-row split-context tiles with few
-// context partitions).  With a host copy of cu_q_lens the planner instead
-// launches each class over the range of sequences that holds it (pointers of
-// the tables offset to the range's first sequence), planned for that class
-// alone; a sequence of the other class inside the range has no rows there.
-// Each launch writes only its own sequences' rows of `out`.
+// that may mix decode-sized requests (grouped rows G * q_len <= kSmallRows:
+// one row tile of the split-context kernel) with prefill-sized ones.  Planned
+// for its longest query, such a call would give every decode sequence the
+// prefill kernel's 128-row tiles (or, in F32, 32-row split-context tiles with
+// few context partitions).  Instead:
+//   launch 0, the split-context kernel planned for the decode shape, over the
+//     range of sequences [lo, hi] that holds the decode class (the whole call
+//     without hints), computing the sequences of that range whose device q_len
+//     is at most its planned q_len (qmax);
+//   launch 1, the prefill kernel planned for max_q_len, over every sequence,
+//     computing every sequence that launch 0 does not (outside [lo, hi], or
+//     with q_len > qmax); key splits, and their partial slots, only for the
+//     range that holds the prefill class.
+// Both launches decide from the device q_len, so each sequence is computed by
+// exactly one of them whatever the host hints say: hints only shape the plans
+// (with cu_q_lens_host a batch of one class runs as one unfiltered launch, and
+// the class ranges and counts size each launch; seq_lens_host sizes the
+// context splits), and a stale hint costs speed, never rows.
 constexpr int kSmallRows = 32;
 
 struct CallPlan {
@@ -546,52 +581,88 @@ CallPlan make_call_plan(const mvr_paged_attention_args* a) {
   c.part[0] = *a;
   c.plan[0] = make_plan(a);
   c.total = c.plan[0].partial_bytes;
+  const int group = a->num_q_heads / a->num_kv_heads;
+  const int small_q = kSmallRows / group; // largest q_len of the small class (0: no such class)
+  if (a->num_seqs < 2 || small_q < 1 || a->max_q_len <= small_q) return c;
+  const bool page_pow2 = (a->page_size & (a->page_size - 1)) == 0;
+  if (!c.plan[0].prefill || !page_pow2) return c; // launch 1 needs the prefill kernel
   const int32_t* cu = a->cu_q_lens_host;
   const int32_t* sl = a->seq_lens_host;
-  if (!cu || a->num_seqs < 2 || (int64_t)a->max_q_len * (a->num_q_heads / a->num_kv_heads) <= kSmallRows) return c;
-  const int group = a->num_q_heads / a->num_kv_heads;
-  int first[2] = {-1, -1}, last[2] = {-1, -1}, qmin[2] = {INT32_MAX, INT32_MAX}, qmax[2] = {0, 0}, lmax[2] = {0, 0};
+  int first[2] = {-1, -1}, last[2] = {-1, -1}, count[2] = {0, 0}, lmax[2] = {0, 0}, qmax = 0;
   int64_t lsum[2] = {0, 0};
-  for (int s = 0; s < a->num_seqs; s++) {
+  bool hinted = cu != nullptr;
+  for (int s = 0; hinted && s < a->num_seqs; s++) {
     const int q = cu[s + 1] - cu[s];
     const int L = sl ? sl[s] : a->max_seq_len;
-    // Hints that break the call's own bounds are not used (the device tables
+    // Hints that break the call's own bounds are ignored (the device tables
     // are what the kernels read; mvr_paged_attention_validate reports them).
-    if (q < 1 || q > a->max_q_len || L < q || L > a->max_seq_len) return c;
-    const int k = (int64_t)group * q <= kSmallRows ? 0 : 1;
+    if (q < 1 || q > a->max_q_len || L < q || L > a->max_seq_len) {
+      hinted = false;
+      break;
+    }
+    const int k = q <= small_q ? 0 : 1;
     if (first[k] < 0) first[k] = s;
     last[k] = s;
-    qmin[k] = q < qmin[k] ? q : qmin[k];
-    qmax[k] = q > qmax[k] ? q : qmax[k];
-    lmax[k] = L > lmax[k] ? L : lmax[k];
+    count[k]++;
+    if (k == 0 && q > qmax) qmax = q;
     lsum[k] += L;
+    if (L > lmax[k]) lmax[k] = L;
   }
-  if (first[0] < 0 || first[1] < 0) return c; // one class: one launch
+  if (hinted && (count[0] == 0 || count[1] == 0)) return c; // one class: one unfiltered launch
+  if (!hinted) {
+    // Without hints the small class is the decode shape, up to 16 grouped
+    // rows (one 16-row tile, the block-merge plans); longer queries,
+    // speculative verification included, go to launch 1.
+    qmax = 16 / group >= 1 ? 16 / group : small_q;
+    first[0] = first[1] = 0;
+    last[0] = last[1] = a->num_seqs - 1;
+  }
   c.n = 2;
-  size_t off = 0;
-  for (int k = 0; k < 2; k++) {
-    mvr_paged_attention_args& p = c.part[k];
-    p = *a;
-    const int f = first[k];
-    p.num_seqs = last[k] - f + 1;
-    // (null tables only when sizing a repacked call's workspace)
-    p.block_tables = a->block_tables ? a->block_tables + (int64_t)f * a->max_pages_per_seq : nullptr;
-    p.seq_lens = a->seq_lens ? a->seq_lens + f : nullptr;
-    p.cu_q_lens = a->cu_q_lens ? a->cu_q_lens + f : nullptr; // q_start stays the whole call's packed index
-    p.seq_lens_host = sl ? sl + f : nullptr;
-    p.cu_q_lens_host = cu + f;
-    p.max_q_len = qmax[k];
-    p.max_seq_len = sl ? lmax[k] : a->max_seq_len;
-    // The range may hold sequences of the other class (no rows here); the
-    // hint counts this class's keys only.
-    p.sum_seq_lens = sl ? lsum[k] : 0;
-    if (p.sum_seq_lens > (int64_t)p.max_seq_len * p.num_seqs) p.sum_seq_lens = 0;
-    c.plan[k] = make_plan(&p);
-    c.extras[k].class_q_min = qmin[k];
-    c.extras[k].class_q_max = qmax[k];
-    c.offset[k] = off;
-    off += align_up(c.plan[k].partial_bytes, 256);
+  // Launch 0: the decode range, its sequences at the call's bounds (the
+  // kernels clamp a device seq_len to max_seq_len).
+  mvr_paged_attention_args& p0 = c.part[0];
+  p0 = *a;
+  const int f = first[0];
+  p0.num_seqs = last[0] - f + 1;
+  // (null tables only when sizing a repacked call's workspace)
+  p0.block_tables = a->block_tables ? a->block_tables + (int64_t)f * a->max_pages_per_seq : nullptr;
+  p0.seq_lens = a->seq_lens ? a->seq_lens + f : nullptr;
+  p0.cu_q_lens = a->cu_q_lens ? a->cu_q_lens + f : nullptr; // q_start stays the whole call's packed index
+  p0.seq_lens_host = nullptr;
+  p0.cu_q_lens_host = nullptr;
+  p0.max_q_len = qmax;
+  LiveSeqs live0;
+  if (hinted) {
+    live0.count = count[0];
+    if (sl) live0.max_seq_len = lmax[0];
+    p0.sum_seq_lens = sl ? lsum[0] : 0; // this class's keys (a speed hint)
   }
+  c.plan[0] = make_plan(&p0, /*allow_prefill=*/false, live0);
+  c.extras[0].class_q_min = 1;
+  c.extras[0].class_q_max = qmax;
+  // Launch 1: every sequence that launch 0 leaves.
+  mvr_paged_attention_args& p1 = c.part[1];
+  p1 = *a;
+  p1.seq_lens_host = nullptr;
+  p1.cu_q_lens_host = nullptr;
+  LiveSeqs live1;
+  if (hinted) {
+    live1.count = count[1];
+    if (sl) live1.max_seq_len = lmax[1];
+    live1.split_count = last[1] - first[1] + 1;
+    p1.sum_seq_lens = sl ? lsum[1] : 0;
+  }
+  c.plan[1] = make_plan(&p1, true, live1, /*force_prefill=*/true);
+  LaunchExtras& e1 = c.extras[1];
+  e1.skip_seq_lo = first[0];
+  e1.skip_seq_hi = last[0];
+  e1.skip_q_max = qmax;
+  if (live1.split_count > 0 && live1.split_count < a->num_seqs) {
+    e1.split_seq_lo = first[1];
+    e1.split_seq_count = (int32_t)live1.split_count;
+  }
+  c.offset[0] = 0;
+  c.offset[1] = align_up(c.plan[0].partial_bytes, 256);
   c.total = c.offset[1] + c.plan[1].partial_bytes;
   return c;
 }
@@ -905,6 +976,17 @@ static int checked_attention_tables(const mvr_paged_attention_args* a) {
       !copy_table(a->seq_lens, (size_t)a->num_seqs, st, sl) ||
       !copy_table(a->cu_q_lens, (size_t)a->num_seqs + 1, st, cu))
     return fail(MVR_E_HIP, "checked mode: copying the device tables to the host failed");
+  // The host hints must hold the device tables' values (they shape the plan).
+  if (a->seq_lens_host && !sl.empty())
+    for (int s = 0; s < a->num_seqs; s++)
+      if (a->seq_lens_host[s] != sl[s])
+        return fail(MVR_E_INVALID_ARGUMENT, "seq_lens_host[%d] = %d differs from the device seq_lens (%d)", s,
+                    a->seq_lens_host[s], sl[s]);
+  if (a->cu_q_lens_host && !cu.empty())
+    for (int s = 0; s <= a->num_seqs; s++)
+      if (a->cu_q_lens_host[s] != cu[s])
+        return fail(MVR_E_INVALID_ARGUMENT, "cu_q_lens_host[%d] = %d differs from the device cu_q_lens (%d)", s,
+                    a->cu_q_lens_host[s], cu[s]);
   return mvr_paged_attention_validate(a, ptr_or_null(bt), ptr_or_null(sl), ptr_or_null(cu));
 }
 

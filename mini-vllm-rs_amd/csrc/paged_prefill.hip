@@ -116,7 +116,7 @@ __device__ __forceinline__ SeqRows load_rows(const PrefillParams& p, int b) {
     s.q_len = p.single_q_len;
   }
   // Another launch's sequence: no rows here (its blocks exit at once).
-  if (s.q_len < p.class_q_min || (p.class_q_max > 0 && s.q_len > p.class_q_max)) s.q_len = 0;
+  if (s.q_len <= p.skip_q_max && b >= p.skip_seq_lo && b <= p.skip_seq_hi) s.q_len = 0;
   if (p.key_end) { // cascade prefix pass: every row sees every key before key_end
     s.key_end = p.key_end[b];
     s.seq_len = s.key_end + s.q_len;
@@ -215,6 +215,11 @@ __global__ __launch_bounds__(kWaves * 64, 1) void paged_prefill_kernel(PrefillPa
   const int h = pair % p.num_kv_heads;
   const int b = pair / p.num_kv_heads;
   const int split = local % p.kv_splits;
+  // Sequences outside the split range run unsplit (split 0 takes every key).
+  const bool split_here =
+      p.split_seq_count == 0 || (b >= p.split_seq_lo && b - p.split_seq_lo < p.split_seq_count);
+  const int kv_splits = split_here ? p.kv_splits : 1;
+  if (split >= kv_splits) return; // whole block: uniform exit before any barrier
   const SeqRows s = load_rows(p, b);
   // Longest first: a tile's causal key range grows with the query positions
   // of its rows, so the pair's tiles are dispatched in decreasing order of
@@ -240,10 +245,11 @@ __global__ __launch_bounds__(kWaves * 64, 1) void paged_prefill_kernel(PrefillPa
   const int rows = p.group_size * s.q_len;
   const int n_tiles = block_key_tiles<TT>(s, p.group_size, rt);
   if (n_tiles == 0) return; // whole block: uniform exit before any barrier
-  const int tiles_per_split = (n_tiles + p.kv_splits - 1) / p.kv_splits;
+  const int tiles_per_split = (n_tiles + kv_splits - 1) / kv_splits;
   const int j0 = split * tiles_per_split;
   const int j1 = min(j0 + tiles_per_split, n_tiles);
-  const int64_t slot = (int64_t)((b * p.num_kv_heads + h) * p.row_tiles + rt) * p.kv_splits + split;
+  const int64_t slot =
+      (int64_t)(((b - p.split_seq_lo) * p.num_kv_heads + h) * p.row_tiles + rt) * p.kv_splits + split; // kv_splits > 1
 
   // This lane's query row.
   const int rho = rt * kBlockRows + rw * kRowsPerWave + (l & 31);
@@ -675,7 +681,7 @@ __global__ __launch_bounds__(kWaves * 64, 1) void paged_prefill_kernel(PrefillPa
       }
     };
     if (!valid) return;
-    if (p.kv_splits > 1) {
+    if (kv_splits > 1) {
       const int64_t prow = slot * kBlockRows + rw * kRowsPerWave + (l & 31);
       put(p.partial_o + prow * D, 1.f);
       if (hh == 0) {
@@ -694,7 +700,7 @@ __global__ __launch_bounds__(kWaves * 64, 1) void paged_prefill_kernel(PrefillPa
     return;
   }
   // Lane holds O^T[d][rho] for d = 32n + 8*(e/4) + 4*hh + e%4.
-  if (p.kv_splits == 1) {
+  if (kv_splits == 1) {
     if (valid && p.state_o) {
       const float inv = 1.f / ltot;
       const int64_t srow = (int64_t)(h * p.group_size + r) * p.state_tokens + s.q_start + i;
@@ -759,13 +765,13 @@ __global__ __launch_bounds__(256) void prefill_merge_kernel(PrefillParams p) {
   constexpr int kPer = D / 64;
   constexpr int kMergeRows = merge_rows<D>();
   constexpr int kBlocksPerTile = kBlockRows / (kMergeWaves * kMergeRows);
-  const int tile = blockIdx.x / kBlocksPerTile; // (b, h, rt)
+  const int tile = blockIdx.x / kBlocksPerTile; // (b - split_seq_lo, h, rt)
   const int lr0 = ((blockIdx.x % kBlocksPerTile) * kMergeWaves + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6)) *
                   kMergeRows;
   const int l = threadIdx.x & 63;
   const int rt = tile % p.row_tiles;
   const int h = (tile / p.row_tiles) % p.num_kv_heads;
-  const int b = tile / (p.row_tiles * p.num_kv_heads);
+  const int b = p.split_seq_lo + tile / (p.row_tiles * p.num_kv_heads);
   const int splits = min(p.kv_splits, kMaxSplits);
   const int64_t prow0 = (int64_t)tile * p.kv_splits * kBlockRows + lr0; // split j, row r: prow0 + j * kBlockRows + r
   float mj_raw[kMergeRows], lj_raw[kMergeRows], v[kMergeRows][kMaxSplits][kPer];
@@ -841,9 +847,11 @@ hipError_t launch_typed(const PrefillParams& params, hipStream_t stream) {
   hipLaunchKernelGGL((paged_prefill_kernel<D, T, TT>), dim3((unsigned)blocks), dim3(kWaves * 64), 0, stream, params);
   hipError_t err = hipGetLastError();
   if (err != hipSuccess || params.kv_splits == 1) return err;
-  hipLaunchKernelGGL((prefill_merge_kernel<D, T, TT>), dim3(pairs * params.row_tiles * (kBlockRows / (kMergeWaves * merge_rows<D>()))),
-                     dim3(256), 0,
-                     stream, params);
+  const int64_t split_pairs =
+      (int64_t)(params.split_seq_count ? params.split_seq_count : params.num_seqs) * params.num_kv_heads;
+  hipLaunchKernelGGL((prefill_merge_kernel<D, T, TT>),
+                     dim3((unsigned)(split_pairs * params.row_tiles * (kBlockRows / (kMergeWaves * merge_rows<D>())))),
+                     dim3(256), 0, stream, params);
   return hipGetLastError();
 }
 

@@ -34,9 +34,14 @@ struct PrefillParams {
   float* state_o;   // [q head][state_tokens][D]
   float* state_lse; // [q head][state_tokens]
   int32_t state_tokens;
-  // Sequences with q_len outside [class_q_min, class_q_max] (0 = no upper
-  // bound) belong to another launch of the same call and are skipped.
-  int32_t class_q_min, class_q_max;
+  // Sequences b in [skip_seq_lo, skip_seq_hi] with q_len <= skip_q_max (0:
+  // none) belong to another launch of the same call and are skipped.
+  int32_t skip_seq_lo, skip_seq_hi, skip_q_max;
+  // Key splits (kv_splits > 1) and their partial slots only for sequences
+  // [split_seq_lo, split_seq_lo + split_seq_count) (count 0: every sequence);
+  // the others run unsplit.  Partial slot of (b, h, rt, split):
+  // (((b - split_seq_lo) * num_kv_heads + h) * row_tiles + rt) * kv_splits + split.
+  int32_t split_seq_lo, split_seq_count;
 };
 
 // f32: F32 Q/K/V/out (v_mfma_f32_32x32x2_f32); otherwise F16.

@@ -206,9 +206,20 @@ pub fn paged_attention_noalloc(args: &MvrPagedAttentionArgs) -> candle_core::Res
     check(unsafe { mvr_paged_attention_noalloc(args) })
 }
 
-/// The checks of common.rs:447-454 and :776-781 on host copies of the tables (no launch).
+/// The checks of common.rs:447-454 and :776-781 on host copies of the tables (no launch).  The slices must hold
+/// the whole tables the arguments describe (the library reads that many entries), else this returns an error
+/// without calling it.
 pub fn validate(args: &MvrPagedAttentionArgs, block_tables: &[i32], seq_lens: &[i32], cu_q_lens: &[i32])
     -> candle_core::Result<()> {
+    let n = args.num_seqs.max(0) as usize;
+    let pages = n.saturating_mul(args.max_pages_per_seq.max(0) as usize);
+    if block_tables.len() < pages || seq_lens.len() < n || cu_q_lens.len() < n + 1 {
+        candle_core::bail!(
+            "validate: tables shorter than the arguments describe (block_tables {} < {}, seq_lens {} < {} or \
+             cu_q_lens {} < {})",
+            block_tables.len(), pages, seq_lens.len(), n, cu_q_lens.len(), n + 1
+        );
+    }
     check(unsafe { mvr_paged_attention_validate(args, block_tables.as_ptr(), seq_lens.as_ptr(), cu_q_lens.as_ptr()) })
 }
 

@@ -146,6 +146,15 @@ def _checked_child(out_path):
     bad_cu = t["cu_q_lens"].clone()
     bad_cu[4] = bad_cu[3]  # an empty request
     results["empty"] = rc_of(cu_q_lens=bad_cu)
+    # host hints that differ from the device tables (they would only shape the plan: checked mode reports them)
+    for key, kw in (("stale_seq_lens", dict(seq_lens_host=w.seq_lens + np.int32(1), cu_q_lens_host=w.cu_q_lens)),
+                    ("stale_cu_q_lens", dict(cu_q_lens_host=np.arange(w.num_seqs + 1, dtype=np.int32) * 2))):
+        try:
+            M.paged_attention(t["q"], t["key_pool"], t["value_pool"], t["block_tables"], t["seq_lens"],
+                              t["cu_q_lens"], max_q_len=w.max_q_len, max_seq_len=w.max_seq_len, **kw)
+            results[key] = (0, "")
+        except M.MvrError as e:
+            results[key] = (e.code, e.message)
     # rope + append writing a page outside the pool
     cos, sin = W.rope_tables(64, 10000.0, w.max_seq_len)
     q = t["q"]
@@ -225,6 +234,10 @@ def test_checked_mode_reports_broken_tables_and_runs_valid_calls():
         assert int(c["seq_len"][0]) == M.MVR_E_INVALID_ARGUMENT and "max_seq_len" in str(c["seq_len_msg"][0])
         assert int(c["page_id"][0]) == M.MVR_E_PAGE_ID and "outside a pool" in str(c["page_id_msg"][0])
         assert int(c["empty"][0]) == M.MVR_E_INVALID_ARGUMENT and "at least one token" in str(c["empty_msg"][0])
+        assert int(c["stale_seq_lens"][0]) == M.MVR_E_INVALID_ARGUMENT and "seq_lens_host" in str(
+            c["stale_seq_lens_msg"][0])
+        assert int(c["stale_cu_q_lens"][0]) == M.MVR_E_INVALID_ARGUMENT and "cu_q_lens_host" in str(
+            c["stale_cu_q_lens_msg"][0])
         assert int(c["rope_page"][0]) == M.MVR_E_PAGE_ID
         assert int(c["cascade_page"][0]) == M.MVR_E_INVALID_ARGUMENT and "differs" in str(c["cascade_page_msg"][0])
 

@@ -106,22 +106,6 @@ def test_noalloc_equals_workspace_call_on_every_plan(case):
     assert torch.equal(n, r)
 
 
-def test_noalloc_refuses_calls_larger_than_its_scratch():
-    """A page size of 5 repacks the batch's K/V into the scratch: 64 sequences of 8K tokens need ~2 GiB, more
-    than the static scratch holds, so the call returns MVR_E_WORKSPACE before launching anything."""
-    lib = M.load_library()
-    a = M.PagedAttentionArgs()
-    a.dtype, a.num_seqs, a.num_q_heads, a.num_kv_heads, a.head_dim = M.DTYPE_F16, 64, 32, 8, 128
-    a.page_size, a.num_pages, a.max_pages_per_seq, a.max_q_len, a.max_seq_len = 5, 1 << 20, 1640, 1, 8192
-    fake = 1 << 20
-    a.q = a.key_pool = a.value_pool = a.block_tables = a.seq_lens = a.cu_q_lens = a.out = fake
-    a.q_stride_head, a.q_stride_token, a.out_stride_head, a.out_stride_token = 64 * 128, 128, 64 * 128, 128
-    assert M.workspace_size(a) > M.NOALLOC_SCRATCH_BYTES
-    rc = lib.mvr_paged_attention_noalloc(ctypes.byref(a))
-    assert rc == M.MVR_E_WORKSPACE
-    assert "static scratch" in lib.mvr_last_error().decode()
-
-
 def test_noalloc_calls_leave_free_device_memory_unchanged():
     w = W.llama3_8b_spec_verify_f16()
     t = W.device_tensors(w, None, seed=8)
