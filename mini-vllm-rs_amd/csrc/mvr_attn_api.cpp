@@ -426,9 +426,10 @@ namespace {
 struct LaunchExtras {
   int32_t class_q_min = 0, class_q_max = 0; // split-context kernel: sequences outside [min, max] (max 0: unbounded) are skipped
   // Prefill kernel: sequences in [skip_seq_lo, skip_seq_hi] with q_len <= skip_q_max (0: none) are skipped;
-  // key splits only for [split_seq_lo, split_seq_lo + split_seq_count) (count 0: all).
+  // the main grid (key splits included) covers [seq_lo, seq_lo + seq_count) (count 0: all), and one
+  // catch-up block per sequence of [catch_lo, catch_lo + catch_count) outside it computes that sequence unsplit.
   int32_t skip_seq_lo = 0, skip_seq_hi = -1, skip_q_max = 0;
-  int32_t split_seq_lo = 0, split_seq_count = 0;
+  int32_t seq_lo = 0, seq_count = 0, catch_lo = 0, catch_count = 0;
   const int32_t* key_begin = nullptr; // suffix pass: first key of each sequence
   const int32_t* key_end = nullptr;   // prefix pass: keys [0, key_end) of each group
   float* state_o = nullptr;           // normalised fp32 rows instead of `out`
@@ -463,7 +464,7 @@ int launch_planned(const mvr_paged_attention_args* a, const mvr::PagedAttentionP
     f.out_stride_head = a->out_stride_head;
     f.out_stride_token = a->out_stride_token;
     if (plan.partial_bytes) {
-      const size_t prow = (size_t)(cp.split_seq_count ? cp.split_seq_count : a->num_seqs) * a->num_kv_heads *
+      const size_t prow = (size_t)(cp.seq_count ? cp.seq_count : a->num_seqs) * a->num_kv_heads *
                           plan.row_tiles * plan.kv_splits * mvr::kPrefillBlockRows;
       char* w = static_cast<char*>(ws);
       f.partial_o = reinterpret_cast<float*>(w);
@@ -487,8 +488,10 @@ int launch_planned(const mvr_paged_attention_args* a, const mvr::PagedAttentionP
     f.skip_seq_lo = cp.skip_seq_lo;
     f.skip_seq_hi = cp.skip_seq_hi;
     f.skip_q_max = cp.skip_q_max;
-    f.split_seq_lo = cp.split_seq_lo;
-    f.split_seq_count = cp.split_seq_count;
+    f.seq_lo = cp.seq_lo;
+    f.seq_count = cp.seq_count;
+    f.catch_lo = cp.catch_lo;
+    f.catch_count = cp.catch_count;
     TraceRange launch("attn-prefill-fused");
     hipError_t err = mvr::launch_paged_prefill(f, a->head_dim, a->dtype == MVR_DTYPE_F32, static_cast<hipStream_t>(a->stream));
     if (err != hipSuccess) return fail(MVR_E_HIP, "kernel launch failed: %s", hipGetErrorString(err));
@@ -556,10 +559,12 @@ int check_workspace(const mvr_paged_attention_args* a, size_t need) {
 //     range of sequences [lo, hi] that holds the decode class (the whole call
 //     without hints), computing the sequences of that range whose device q_len
 //     is at most its planned q_len (qmax);
-//   launch 1, the prefill kernel planned for max_q_len, over every sequence,
-//     computing every sequence that launch 0 does not (outside [lo, hi], or
-//     with q_len > qmax); key splits, and their partial slots, only for the
-//     range that holds the prefill class.
+//   launch 1, the prefill kernel planned for max_q_len, computing every
+//     sequence that launch 0 does not (outside [lo, hi], or with q_len >
+//     qmax): its main grid (key splits and partial slots included) covers the
+//     range that holds the prefill class, and one catch-up block per
+//     sequence covers the rest of [lo, hi] (each exits at once unless a stale
+//     hint put a prefill-sized request there, which it then computes unsplit).
 // Both launches decide from the device q_len, so each sequence is computed by
 // exactly one of them whatever the host hints say: hints only shape the plans
 // (with cu_q_lens_host a batch of one class runs as one unfiltered launch, and
@@ -658,8 +663,13 @@ CallPlan make_call_plan(const mvr_paged_attention_args* a) {
   e1.skip_seq_hi = last[0];
   e1.skip_q_max = qmax;
   if (live1.split_count > 0 && live1.split_count < a->num_seqs) {
-    e1.split_seq_lo = first[1];
-    e1.split_seq_count = (int32_t)live1.split_count;
+    // Main grid over the prefill range; the rest of the decode range gets a
+    // catch-up block per sequence (it exits unless a stale hint put a
+    // prefill-sized request there).
+    e1.seq_lo = first[1];
+    e1.seq_count = (int32_t)live1.split_count;
+    e1.catch_lo = first[0];
+    e1.catch_count = last[0] - first[0] + 1;
   }
   c.offset[0] = 0;
   c.offset[1] = align_up(c.plan[0].partial_bytes, 256);

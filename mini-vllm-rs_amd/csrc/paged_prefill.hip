@@ -166,8 +166,11 @@ struct Tile {
   __device__ static __forceinline__ int kswz(int t) { return t & (kChunksPerRow < 16 ? kChunksPerRow - 1 : 15); }
 };
 
+// One (sequence, kv head, 128-row tile, key split): each step stages one
+// key tile per group, then QK^T, softmax and PV in turn.
 template <int D, typename T, int TT>
-__global__ __launch_bounds__(kWaves * 64, 1) void paged_prefill_kernel(PrefillParams p) {
+__device__ __forceinline__ void prefill_tile_serial(const PrefillParams& p, const SeqRows& s, int b, int h, int rt,
+                                                    int split, int kv_splits) {
   typedef Tile<D, T, TT> TL;
   constexpr bool kF32 = TL::kF32;
   // Key tile of one group per step: TT tokens = kSub S^T blocks of 32 tokens.
@@ -196,60 +199,14 @@ __global__ __launch_bounds__(kWaves * 64, 1) void paged_prefill_kernel(PrefillPa
   const int grp = wave / kRowWaves; // key tiles j0 + 2i + grp
   const int hh = l >> 5;            // lane half: 0 or 1
 
-  // XCD-aware decode of the block index: block x runs on XCD x % 8; all
-  // blocks of one (sequence, kv head) pair sit on the same XCD.
-  // With fewer pairs than XCDs, plain linear order keeps every XCD busy.
-  const int x = blockIdx.x;
-  const int per_pair = p.row_tiles * p.kv_splits;
-  const int pairs = p.num_seqs * p.num_kv_heads;
-  int pair, local;
-  if (pairs >= kXcds) {
-    const int k_on_xcd = x / kXcds;
-    pair = (x % kXcds) + kXcds * (k_on_xcd / per_pair);
-    local = k_on_xcd % per_pair;
-  } else {
-    pair = x / per_pair;
-    local = x % per_pair;
-  }
-  if (pair >= pairs) return;
-  const int h = pair % p.num_kv_heads;
-  const int b = pair / p.num_kv_heads;
-  const int split = local % p.kv_splits;
-  // Sequences outside the split range run unsplit (split 0 takes every key).
-  const bool split_here =
-      p.split_seq_count == 0 || (b >= p.split_seq_lo && b - p.split_seq_lo < p.split_seq_count);
-  const int kv_splits = split_here ? p.kv_splits : 1;
-  if (split >= kv_splits) return; // whole block: uniform exit before any barrier
-  const SeqRows s = load_rows(p, b);
-  // Longest first: a tile's causal key range grows with the query positions
-  // of its rows, so the pair's tiles are dispatched in decreasing order of
-  // work.  When q_len is a multiple of the tile (rows r*q_len + i, tile j of
-  // query head r covers positions 128j .. 128j+127), that is position tile j
-  // descending across all query heads of the group, and block indices past
-  // the sequence's own tiles keep their index (no rows: they exit);
-  // otherwise row tiles in reverse.  Either way a bijection of [0, row_tiles):
-  // the same blocks in another order, bit for bit.  Measured on
-  // fresh prompts: Llama-3-8B 1 x 2048 F16 75.3 (in order) -> 70.7 (reverse)
-  // -> 58.0 us (by position), F32 512.1 -> 480.6 -> 325.9, Qwen2-7B 1 x 8192
-  // 667.7 -> 632.6 -> 517.4; chunks on a long prefix level.
-  int rt;
-  {
-    const int idx = local / p.kv_splits;
-    const int tq = s.q_len / kBlockRows; // tiles per query head
-    if (s.q_len > 0 && s.q_len % kBlockRows == 0) {
-      rt = idx < p.group_size * tq ? (idx % p.group_size) * tq + (tq - 1 - idx / p.group_size) : idx;
-    } else {
-      rt = p.row_tiles - 1 - idx;
-    }
-  }
   const int rows = p.group_size * s.q_len;
   const int n_tiles = block_key_tiles<TT>(s, p.group_size, rt);
-  if (n_tiles == 0) return; // whole block: uniform exit before any barrier
+  if (n_tiles == 0) return; // whole block: uniform return before any barrier
   const int tiles_per_split = (n_tiles + kv_splits - 1) / kv_splits;
   const int j0 = split * tiles_per_split;
   const int j1 = min(j0 + tiles_per_split, n_tiles);
   const int64_t slot =
-      (int64_t)(((b - p.split_seq_lo) * p.num_kv_heads + h) * p.row_tiles + rt) * p.kv_splits + split; // kv_splits > 1
+      (int64_t)(((b - p.seq_lo) * p.num_kv_heads + h) * p.row_tiles + rt) * p.kv_splits + split; // kv_splits > 1
 
   // This lane's query row.
   const int rho = rt * kBlockRows + rw * kRowsPerWave + (l & 31);
@@ -742,6 +699,81 @@ __global__ __launch_bounds__(kWaves * 64, 1) void paged_prefill_kernel(PrefillPa
   }
 }
 
+// Main grid: block x covers (sequence, kv head, row tile, key split) of the
+// main range.  XCD-aware decode: block x runs on XCD x % 8 and all blocks of
+// one (sequence, kv head) pair sit on the same XCD, so their shared K/V stays
+// in that XCD's L2 (with fewer pairs than XCDs, plain linear order keeps
+// every XCD busy).  Catch-up blocks follow the main grid.
+template <int D, typename T>
+__device__ __forceinline__ void prefill_tile(const PrefillParams& p, const SeqRows& s, int b, int h, int rt, int split,
+                                             int kv_splits) {
+  prefill_tile_serial<D, T, sizeof(T) == 4 ? 32 : 64>(p, s, b, h, rt, split, kv_splits);
+}
+
+__host__ __device__ __forceinline__ int64_t prefill_main_blocks(const PrefillParams& p) {
+  const int64_t pairs = (int64_t)(p.seq_count ? p.seq_count : p.num_seqs) * p.num_kv_heads;
+  const int64_t per_pair = (int64_t)p.row_tiles * p.kv_splits;
+  return pairs >= kXcds ? kXcds * ((pairs + kXcds - 1) / kXcds) * per_pair : pairs * per_pair;
+}
+
+template <int D, typename T>
+__global__ __launch_bounds__(kWaves * 64, 1) void paged_prefill_kernel(PrefillParams p) {
+  const int x = blockIdx.x;
+  const int main_seqs = p.seq_count ? p.seq_count : p.num_seqs;
+  const int main_blocks = (int)prefill_main_blocks(p);
+  if (x >= main_blocks) {
+    // Catch-up block: every (kv head, row tile) of one sequence, unsplit.
+    const int b = p.catch_lo + (x - main_blocks);
+    if (b >= p.seq_lo && b < p.seq_lo + main_seqs) return; // the main grid covers it
+    const SeqRows s = load_rows(p, b);
+    if (s.q_len <= 0) return;
+    for (int h = 0; h < p.num_kv_heads; h++)
+      for (int rt = 0; rt < p.row_tiles; rt++) {
+        prefill_tile<D, T>(p, s, b, h, rt, 0, 1);
+        __syncthreads(); // group 0's hand-off reads end before the next tile refills the stages
+      }
+    return;
+  }
+  const int per_pair = p.row_tiles * p.kv_splits;
+  const int pairs = main_seqs * p.num_kv_heads;
+  int pair, local;
+  if (pairs >= kXcds) {
+    const int k_on_xcd = x / kXcds;
+    pair = (x % kXcds) + kXcds * (k_on_xcd / per_pair);
+    local = k_on_xcd % per_pair;
+  } else {
+    pair = x / per_pair;
+    local = x % per_pair;
+  }
+  if (pair >= pairs) return;
+  const int h = pair % p.num_kv_heads;
+  const int b = p.seq_lo + pair / p.num_kv_heads;
+  const int split = local % p.kv_splits;
+  const SeqRows s = load_rows(p, b);
+  // Longest first: a tile's causal key range grows with the query positions
+  // of its rows, so the pair's tiles are dispatched in decreasing order of
+  // work.  When q_len is a multiple of the tile (rows r*q_len + i, tile j of
+  // query head r covers positions 128j .. 128j+127), that is position tile j
+  // descending across all query heads of the group, and block indices past
+  // the sequence's own tiles keep their index (no rows: they exit);
+  // otherwise row tiles in reverse.  Either way a bijection of [0, row_tiles):
+  // the same blocks in another order, bit for bit.  Measured on
+  // fresh prompts: Llama-3-8B 1 x 2048 F16 75.3 (in order) -> 70.7 (reverse)
+  // -> 58.0 us (by position), F32 512.1 -> 480.6 -> 325.9, Qwen2-7B 1 x 8192
+  // 667.7 -> 632.6 -> 517.4; chunks on a long prefix level.
+  int rt;
+  {
+    const int idx = local / p.kv_splits;
+    const int tq = s.q_len / kBlockRows; // tiles per query head
+    if (s.q_len > 0 && s.q_len % kBlockRows == 0) {
+      rt = idx < p.group_size * tq ? (idx % p.group_size) * tq + (tq - 1 - idx / p.group_size) : idx;
+    } else {
+      rt = p.row_tiles - 1 - idx;
+    }
+  }
+  prefill_tile<D, T>(p, s, b, h, rt, split, p.kv_splits);
+}
+
 // Merges the kv_splits partial results of every block tile:
 //   out = sum_j 2^(m_j - M) o_j / sum_j 2^(m_j - M) l_j.
 // One wavefront per merge_rows<D>() output rows of a tile (a 256-thread
@@ -765,13 +797,13 @@ __global__ __launch_bounds__(256) void prefill_merge_kernel(PrefillParams p) {
   constexpr int kPer = D / 64;
   constexpr int kMergeRows = merge_rows<D>();
   constexpr int kBlocksPerTile = kBlockRows / (kMergeWaves * kMergeRows);
-  const int tile = blockIdx.x / kBlocksPerTile; // (b - split_seq_lo, h, rt)
+  const int tile = blockIdx.x / kBlocksPerTile; // (b - seq_lo, h, rt)
   const int lr0 = ((blockIdx.x % kBlocksPerTile) * kMergeWaves + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6)) *
                   kMergeRows;
   const int l = threadIdx.x & 63;
   const int rt = tile % p.row_tiles;
   const int h = (tile / p.row_tiles) % p.num_kv_heads;
-  const int b = p.split_seq_lo + tile / (p.row_tiles * p.num_kv_heads);
+  const int b = p.seq_lo + tile / (p.row_tiles * p.num_kv_heads);
   const int splits = min(p.kv_splits, kMaxSplits);
   const int64_t prow0 = (int64_t)tile * p.kv_splits * kBlockRows + lr0; // split j, row r: prow0 + j * kBlockRows + r
   float mj_raw[kMergeRows], lj_raw[kMergeRows], v[kMergeRows][kMaxSplits][kPer];
@@ -840,15 +872,11 @@ __global__ __launch_bounds__(256) void prefill_merge_kernel(PrefillParams p) {
 template <int D, typename T>
 hipError_t launch_typed(const PrefillParams& params, hipStream_t stream) {
   constexpr int TT = sizeof(T) == 4 ? 32 : 64;
-  const int pairs = params.num_seqs * params.num_kv_heads;
-  const int per_pair = params.row_tiles * params.kv_splits;
-  const int64_t blocks =
-      pairs >= kXcds ? (int64_t)kXcds * ((pairs + kXcds - 1) / kXcds) * per_pair : (int64_t)pairs * per_pair;
-  hipLaunchKernelGGL((paged_prefill_kernel<D, T, TT>), dim3((unsigned)blocks), dim3(kWaves * 64), 0, stream, params);
+  const int64_t blocks = prefill_main_blocks(params) + params.catch_count;
+  hipLaunchKernelGGL((paged_prefill_kernel<D, T>), dim3((unsigned)blocks), dim3(kWaves * 64), 0, stream, params);
   hipError_t err = hipGetLastError();
   if (err != hipSuccess || params.kv_splits == 1) return err;
-  const int64_t split_pairs =
-      (int64_t)(params.split_seq_count ? params.split_seq_count : params.num_seqs) * params.num_kv_heads;
+  const int64_t split_pairs = (int64_t)(params.seq_count ? params.seq_count : params.num_seqs) * params.num_kv_heads;
   hipLaunchKernelGGL((prefill_merge_kernel<D, T, TT>),
                      dim3((unsigned)(split_pairs * params.row_tiles * (kBlockRows / (kMergeWaves * merge_rows<D>())))),
                      dim3(256), 0, stream, params);

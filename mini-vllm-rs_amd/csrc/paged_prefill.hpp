@@ -37,11 +37,16 @@ struct PrefillParams {
   // Sequences b in [skip_seq_lo, skip_seq_hi] with q_len <= skip_q_max (0:
   // none) belong to another launch of the same call and are skipped.
   int32_t skip_seq_lo, skip_seq_hi, skip_q_max;
-  // Key splits (kv_splits > 1) and their partial slots only for sequences
-  // [split_seq_lo, split_seq_lo + split_seq_count) (count 0: every sequence);
-  // the others run unsplit.  Partial slot of (b, h, rt, split):
-  // (((b - split_seq_lo) * num_kv_heads + h) * row_tiles + rt) * kv_splits + split.
-  int32_t split_seq_lo, split_seq_count;
+  // Main grid: one block per (sequence, kv head, row tile, key split) for the
+  // sequences [seq_lo, seq_lo + seq_count) (count 0: every sequence).  Partial
+  // slot of (b, h, rt, split): (((b - seq_lo) * num_kv_heads + h) * row_tiles
+  // + rt) * kv_splits + split.
+  int32_t seq_lo, seq_count;
+  // Catch-up blocks after the main grid: one per sequence of [catch_lo,
+  // catch_lo + catch_count) outside the main range, each computing every
+  // (kv head, row tile) of its sequence unsplit (normally none has rows: they
+  // cover sequences that host hints placed in another launch's class).
+  int32_t catch_lo, catch_count;
 };
 
 // f32: F32 Q/K/V/out (v_mfma_f32_32x32x2_f32); otherwise F16.
