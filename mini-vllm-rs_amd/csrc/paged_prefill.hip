@@ -314,9 +314,9 @@ __device__ __forceinline__ void prefill_tile_serial(const PrefillParams& p, cons
   constexpr int kLoadsPerStage = 2 * TL::kChunksPerThread; // per lane
   T* const k_st[4] = {k_lds0, k_lds1, k_lds2, k_lds3};
   T* const v_st[4] = {v_lds0, v_lds1, v_lds2, v_lds3};
-  // O hand-off through the first two K and V stages: part n (16 values per
-  // lane) of row wave rw at float (((n * 4 + rw) * 16 + e) * 64 + lane) of
-  // their concatenation, 1024 floats per (n, rw).
+  // O hand-off through the idle stages: part n (16 values per lane) of row
+  // wave rw in 1024 floats from float (n * 4 + rw) * 1024 of the stages'
+  // concatenation, as float4 [e / 4][lane] (16-byte LDS accesses).
   constexpr int kStageFloats = TL::kElems * (int)sizeof(T) / 4;
   static_assert((D / 32) * kRowWaves * 1024 <= 4 * kStageFloats, "O hand-off exceeds four stages");
   auto xfer_o = [&](int n) -> float* {
@@ -602,9 +602,10 @@ __device__ __forceinline__ void prefill_tile_serial(const PrefillParams& p, cons
   if (grp == 1) {
 #pragma unroll
     for (int n = 0; n < D / 32; n++) {
-      float* dst = xfer_o(n);
+      float4v* dst = reinterpret_cast<float4v*>(xfer_o(n));
 #pragma unroll
-      for (int e = 0; e < 16; e++) dst[e * 64 + l] = o[n][e];
+      for (int e4 = 0; e4 < 4; e4++)
+        dst[e4 * 64 + l] = float4v{o[n][4 * e4], o[n][4 * e4 + 1], o[n][4 * e4 + 2], o[n][4 * e4 + 3]};
     }
     ml_xfer[rw][0][l] = m;
     ml_xfer[rw][1][l] = lsum;
@@ -618,9 +619,15 @@ __device__ __forceinline__ void prefill_tile_serial(const PrefillParams& p, cons
     const float a0 = m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m - mm);
     const float a1 = m1 == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m1 - mm);
 #pragma unroll
-    for (int n = 0; n < D / 32; n++)
+    for (int n = 0; n < D / 32; n++) {
+      const float4v* src = reinterpret_cast<const float4v*>(xfer_o(n));
 #pragma unroll
-      for (int e = 0; e < 16; e++) o[n][e] = a0 * o[n][e] + a1 * xfer_o(n)[e * 64 + l];
+      for (int e4 = 0; e4 < 4; e4++) {
+        const float4v x = src[e4 * 64 + l];
+#pragma unroll
+        for (int c = 0; c < 4; c++) o[n][4 * e4 + c] = a0 * o[n][4 * e4 + c] + a1 * x[c];
+      }
+    }
     lsum = a0 * lsum + a1 * l1;
     m = mm;
   }
@@ -669,18 +676,43 @@ __device__ __forceinline__ void prefill_tile_serial(const PrefillParams& p, cons
           *reinterpret_cast<float4v*>(dst + 32 * n + 8 * a + 4 * hh) =
               float4v{o[n][4 * a], o[n][4 * a + 1], o[n][4 * a + 2], o[n][4 * a + 3]} * inv;
       if (hh == 0) p.state_lse[srow] = m + __log2f(ltot);
-    } else if (valid) {
-      const float inv = 1.f / ltot;
-      half_t* dst = static_cast<half_t*>(p.out) + (int64_t)(h * p.group_size + r) * p.out_stride_head +
-                    (int64_t)(s.q_start + i) * p.out_stride_token;
+    } else if (!p.state_o) {
+      // The wavefront's 32 rows go through LDS (its own 32 x D slice of the
+      // idle V stage 0: the hand-off used K stages 0 and 1 only), so that the
+      // output is written 16 bytes per lane along whole rows.  Written
+      // straight from the MFMA layout, each store instruction would touch 32
+      // rows 8 bytes at a time: 3.6 of the 47 us of the Qwen2-7B prefill
+      // chunk.  The slice swizzles 16-byte chunks with the row (chunk ^ row %
+      // chunks), so neither the 8-byte writes nor the 16-byte reads collide
+      // in LDS banks.  A wavefront's LDS accesses complete in order, so its
+      // reads see its writes.
+      constexpr int kChunksPerRow = D / 8;
+      static_assert(kF32 || kRowWaves * kRowsPerWave * D <= TL::kElems, "output staging exceeds the V stage");
+      half_t* slice = reinterpret_cast<half_t*>(v_lds0) + rw * kRowsPerWave * D;
+      const float inv = valid ? 1.f / ltot : 0.f;
+      const int row = l & 31;
 #pragma unroll
       for (int n = 0; n < D / 32; n++)
 #pragma unroll
         for (int a = 0; a < 4; a++) {
-          half4 v4 = {(half_t)(o[n][4 * a] * inv), (half_t)(o[n][4 * a + 1] * inv), (half_t)(o[n][4 * a + 2] * inv),
-                      (half_t)(o[n][4 * a + 3] * inv)};
-          *reinterpret_cast<half4*>(dst + 32 * n + 8 * a + 4 * hh) = v4;
+          const half4 v4 = {(half_t)(o[n][4 * a] * inv), (half_t)(o[n][4 * a + 1] * inv),
+                            (half_t)(o[n][4 * a + 2] * inv), (half_t)(o[n][4 * a + 3] * inv)};
+          const int chunk = (4 * n + a) ^ (row & (kChunksPerRow - 1));
+          *reinterpret_cast<half4*>(slice + row * D + chunk * 8 + 4 * hh) = v4;
         }
+      constexpr int kRowsPerRead = 64 / kChunksPerRow;
+      const int cc = l % kChunksPerRow;
+#pragma unroll
+      for (int k = 0; k < kRowsPerWave / kRowsPerRead; k++) {
+        const int rr = k * kRowsPerRead + l / kChunksPerRow; // row of the wavefront's 32
+        const half8 v8 = *reinterpret_cast<const half8*>(slice + rr * D + (cc ^ (rr & (kChunksPerRow - 1))) * 8);
+        const int rho_w = rt * kBlockRows + rw * kRowsPerWave + rr;
+        if (rho_w < rows) {
+          const int rr_r = rho_w / s.q_len, rr_i = rho_w % s.q_len;
+          *reinterpret_cast<half8*>(static_cast<half_t*>(p.out) + (int64_t)(h * p.group_size + rr_r) * p.out_stride_head +
+                                    (int64_t)(s.q_start + rr_i) * p.out_stride_token + cc * 8) = v8;
+        }
+      }
     }
   } else if (valid) {
     const int64_t prow = slot * kBlockRows + rw * kRowsPerWave + (l & 31);
