@@ -21,9 +21,22 @@ sys.path.insert(0, os.path.join(ROOT, "mini-vllm-rs_amd"))
 HBM_PEAK_GBS = 8000.0      # MI355X HBM3E, 8 TB/s
 MFMA_F16_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 MFMA
 MFMA_F32_PEAK_TFLOPS = 157.3   # MI355X dense fp32 MFMA
-# HBM bytes per launch of the split-context kernel, from the FETCH_SIZE / WRITE_SIZE counter runs
-# summarised in this file (line "bytes_per_launch: N").
+# HBM bytes per launch of the headline's kernel, from the FETCH_SIZE / WRITE_SIZE counter runs summarised in
+# this file (line "bytes_per_launch: N"), valid for the kernel sources it names (line "source_sha256: H", the
+# SHA-256 of TRAFFIC_SOURCES concatenated): after any change to them the figure is stale and not reported.
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "paged_attention_decode_b64_ctx8192_f16_hbm_traffic.md")
+TRAFFIC_SOURCES = [os.path.join(ROOT, "mini-vllm-rs_amd", "csrc", f)
+                   for f in ("paged_attention.hip", "paged_attention_kernels.hpp")]
+
+
+def traffic_source_sha256():
+    import hashlib
+
+    h = hashlib.sha256()
+    for f in TRAFFIC_SOURCES:
+        with open(f, "rb") as fh:
+            h.update(fh.read())
+    return h.hexdigest()
 
 
 def log(msg):
@@ -382,12 +395,17 @@ def main():
         del src, dst
         torch.cuda.empty_cache()
 
-    traffic = None
+    traffic, traffic_sha = None, None
     if os.path.exists(TRAFFIC_FILE):
         with open(TRAFFIC_FILE) as f:
             for line in f:
                 if line.startswith("bytes_per_launch:"):
                     traffic = int(line.split(":")[1])
+                elif line.startswith("source_sha256:"):
+                    traffic_sha = line.split(":")[1].strip()
+    if traffic is not None and traffic_sha != traffic_source_sha256():
+        log("[bench] the HBM traffic figure was measured on other kernel sources: not reported")
+        traffic = None
 
     result = {
         "metric": "decode attention us/step + effective KV-read GB/s (% HBM peak), 1 MI355X",

@@ -5,12 +5,15 @@ this test measures what the part actually delivers to the two access
 patterns that matter here (tests/bandwidth/hbm_read_probe.hip): one linear
 pass over 2 GiB, and the same bytes as 4 KiB pages (one KV head's slab of a
 16-token F16 page at head_dim 128) visited in a random order, one wavefront
-per page, as a paged K/V walk reads them.  Each probe runs at several grid
-sizes (10 timed launches each, HIP events) and the best rate counts.  The
-Llama-3-8B batch-64 x 8K F16 decode call (its algorithmic K/V + Q + output
-bytes) must then reach at least 80% of the page-walk ceiling: a loose bar,
-so that the box-to-box spread of either figure cannot fail it, while a plan
-or kernel regression of the headline (it measures above 95%) would.
+per page, as a paged K/V walk reads them.  Each probe is swept over grid
+sizes and bytes in flight (4, 8, 16 loads per thread for the linear pass;
+2, 4, 8 pages per wavefront for the walk), 10 timed launches each (HIP
+events), so that the best rate is a plateau and not a probe that stops
+short of the ceiling.  The Llama-3-8B batch-64 x 8K F16 decode call (its
+algorithmic K/V + Q + output bytes) must then reach at least 80% of the
+page-walk ceiling: a loose bar, so that the box-to-box spread of either
+figure cannot fail it, while a plan or kernel regression of the headline
+would.
 """
 import ctypes
 import os
@@ -29,7 +32,9 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 PROBE = os.path.join(HERE, "bandwidth", "libhbm_read_probe.so")
 BYTES = 2 << 30
 PAGE = 4096
-GRIDS = (1024, 2048, 4096, 8192)
+GRIDS = (1024, 2048, 4096, 8192, 16384)
+STREAM_INFLIGHT = (4, 8, 16)
+WALK_INFLIGHT = (2, 4, 8)
 
 
 @pytest.fixture(scope="module")
@@ -39,9 +44,10 @@ def probe():
     if not os.path.exists(PROBE):
         pytest.fail(f"{PROBE} is missing: build it with `make -C {os.path.dirname(PROBE)}`")
     lib = ctypes.CDLL(PROBE)
-    lib.hbm_stream_read.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p]
+    lib.hbm_stream_read.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p, ctypes.c_int, ctypes.c_int,
+                                    ctypes.c_void_p]
     lib.hbm_page_walk_read.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p, ctypes.c_int,
-                                       ctypes.c_void_p]
+                                       ctypes.c_int, ctypes.c_void_p]
     return lib
 
 
@@ -70,11 +76,20 @@ def test_headline_reaches_the_page_walk_ceiling(probe):
     stream_gbs, walk_gbs = {}, {}
     for grid in GRIDS:
         assert out.numel() >= grid * 256
-        stream_gbs[grid] = _rate(lambda: probe.hbm_stream_read(buf.data_ptr(), BYTES, out.data_ptr(), grid, stream),
-                                 BYTES)
-        walk_gbs[grid] = _rate(lambda: probe.hbm_page_walk_read(buf.data_ptr(), order.data_ptr(), n_pages,
-                                                                out.data_ptr(), grid, stream), BYTES)
-        print(f"[ceiling] grid {grid:5d}: linear {stream_gbs[grid]:7.0f} GB/s, 4 KiB page walk {walk_gbs[grid]:7.0f} GB/s",
+        for k in STREAM_INFLIGHT:
+            rc = []
+            stream_gbs[grid, k] = _rate(lambda: rc.append(probe.hbm_stream_read(buf.data_ptr(), BYTES, out.data_ptr(),
+                                                                                grid, k, stream)), BYTES)
+            assert set(rc) == {0}, rc
+        for k in WALK_INFLIGHT:
+            rc = []
+            walk_gbs[grid, k] = _rate(lambda: rc.append(probe.hbm_page_walk_read(buf.data_ptr(), order.data_ptr(),
+                                                                                 n_pages, out.data_ptr(), grid, k,
+                                                                                 stream)), BYTES)
+            assert set(rc) == {0}, rc
+        print(f"[ceiling] grid {grid:5d}: linear " +
+              ", ".join(f"{k:2d}/thread {stream_gbs[grid, k]:6.0f}" for k in STREAM_INFLIGHT) +
+              " GB/s; page walk " + ", ".join(f"{k}/wave {walk_gbs[grid, k]:6.0f}" for k in WALK_INFLIGHT) + " GB/s",
               flush=True)
     del buf, order, out
     torch.cuda.empty_cache()
