@@ -53,7 +53,7 @@
 extern "C" {
 #endif
 
-#define MVR_ATTN_ABI_VERSION 2
+#define MVR_ATTN_ABI_VERSION 3
 
 /* ActivationDType (src/model_runner/mod.rs:331-351): F32 or F16 only. */
 typedef enum { MVR_DTYPE_F32 = 0, MVR_DTYPE_F16 = 1 } mvr_dtype;
@@ -115,6 +115,13 @@ typedef struct mvr_paged_attention_args {
      only. */
   const int32_t* seq_lens_host;
   const int32_t* cu_q_lens_host;
+  /* Token dimension of q and out (0 = unknown; the bindings fill it from q's shape): cu_q_lens[num_seqs] must
+     not exceed it, and when given it must lie in [num_seqs, num_seqs * max_q_len].  Without cu_q_lens_host it
+     shapes the two launches of a mixed batch: the tokens beyond one per sequence are taken to fill prefill
+     requests of max_q_len each packed after the decodes, and a call whose tokens could fill every sequence
+     that way runs as one prefill launch.  Checked by mvr_paged_attention_validate against the host
+     cu_q_lens and, with MVR_ATTN_CHECKED=true, against the device copy. */
+  int32_t total_q;
 } mvr_paged_attention_args;
 
 /* Bytes of workspace mvr_paged_attention needs for these arguments (depends

@@ -137,6 +137,13 @@ int check_scalars(const mvr_paged_attention_args* a) {
                 (long long)a->sum_seq_lens);
   if (a->max_seq_len < a->max_q_len)
     return fail(MVR_E_INVALID_ARGUMENT, "max_seq_len %d is smaller than max_q_len %d", a->max_seq_len, a->max_q_len);
+  if (a->total_q < 0 || (a->total_q > 0 && (a->total_q < a->num_seqs ||
+                                            a->total_q > (int64_t)a->num_seqs * a->max_q_len)))
+    return fail(MVR_E_INVALID_ARGUMENT, "total_q %d is outside [num_seqs, num_seqs * max_q_len] (0: unknown)",
+                a->total_q);
+  if (a->num_seqs == 1 && !a->cu_q_lens && a->total_q > 0 && a->total_q < a->max_q_len)
+    return fail(MVR_E_INVALID_ARGUMENT, "total_q %d is smaller than max_q_len %d, the q_len of a call without cu_q_lens",
+                a->total_q, a->max_q_len);
   const int64_t pages_needed = (a->max_seq_len + a->page_size - 1) / a->page_size;
   if (a->max_pages_per_seq < pages_needed)
     return fail(MVR_E_PAGES_UNCOVERED,
@@ -192,7 +199,6 @@ mvr::PagedAttentionPlan make_plan(const mvr_paged_attention_args* a, bool allow_
   if (allow_prefill && prefill_enabled && (rows_max > 64 || force_prefill) && page_pow2) {
     plan.prefill = true;
     plan.row_tiles = (int)((rows_max + mvr::kPrefillBlockRows - 1) / mvr::kPrefillBlockRows);
-    const int64_t base_blocks = (int64_t)a->num_seqs * a->num_kv_heads * plan.row_tiles;
     const int64_t live_blocks = n_live * a->num_kv_heads * plan.row_tiles;
     const int key_tiles = (len_live + 31) / 32;
     static const int split_override = env_int("MVR_ATTN_PREFILL_SPLITS", 0);
@@ -557,14 +563,15 @@ int check_workspace(const mvr_paged_attention_args* a, size_t need) {
 // few context partitions).  Instead:
 //   launch 0, the split-context kernel planned for the decode shape, over the
 //     range of sequences [lo, hi] that holds the decode class (the whole call
-//     without hints), computing the sequences of that range whose device q_len
-//     is at most its planned q_len (qmax);
+//     without host tables), computing the sequences of that range whose device
+//     q_len is at most its planned q_len (qmax);
 //   launch 1, the prefill kernel planned for max_q_len, computing every
 //     sequence that launch 0 does not (outside [lo, hi], or with q_len >
 //     qmax): its main grid (key splits and partial slots included) covers the
 //     range that holds the prefill class, and one catch-up block per
 //     sequence covers the rest of [lo, hi] (each exits at once unless a stale
-//     hint put a prefill-sized request there, which it then computes unsplit).
+//     hint or a wrong guess put a prefill-sized request there, which it then
+//     computes unsplit).
 // Both launches decide from the device q_len, so each sequence is computed by
 // exactly one of them whatever the host hints say: hints only shape the plans
 // (with cu_q_lens_host a batch of one class runs as one unfiltered launch, and
@@ -617,10 +624,25 @@ CallPlan make_call_plan(const mvr_paged_attention_args* a) {
   if (!hinted) {
     // Without hints the small class is the decode shape, up to 16 grouped
     // rows (one 16-row tile, the block-merge plans); longer queries,
-    // speculative verification included, go to launch 1.
+    // speculative verification included, go to launch 1.  Launch 0 spans
+    // every sequence.  The plans guess the rest from total_q: the tokens
+    // beyond one per sequence are taken to fill prefill requests of
+    // max_q_len each, packed after the decodes (the order in which
+    // scheduler.rs:258-271 builds a batch).  A call whose tokens could fill
+    // every sequence that way runs as one prefill launch (correct for any
+    // mix, as is the guess: a prefill request outside the guessed tail is
+    // computed unsplit by a catch-up block).
     qmax = 16 / group >= 1 ? 16 / group : small_q;
-    first[0] = first[1] = 0;
-    last[0] = last[1] = a->num_seqs - 1;
+    // Unknown total_q: one prefill request.
+    const int64_t excess = a->total_q > 0 ? (int64_t)a->total_q - a->num_seqs : 0;
+    int64_t n_pref = excess > 0 ? (excess + a->max_q_len - 2) / (a->max_q_len - 1) : 1;
+    if (n_pref >= a->num_seqs) return c;
+    count[0] = a->num_seqs - (int)n_pref;
+    count[1] = (int)n_pref;
+    first[0] = 0;
+    last[0] = a->num_seqs - 1;
+    first[1] = a->num_seqs - (int)n_pref;
+    last[1] = a->num_seqs - 1;
   }
   c.n = 2;
   // Launch 0: the decode range, its sequences at the call's bounds (the
@@ -637,8 +659,8 @@ CallPlan make_call_plan(const mvr_paged_attention_args* a) {
   p0.cu_q_lens_host = nullptr;
   p0.max_q_len = qmax;
   LiveSeqs live0;
+  live0.count = count[0];
   if (hinted) {
-    live0.count = count[0];
     if (sl) live0.max_seq_len = lmax[0];
     p0.sum_seq_lens = sl ? lsum[0] : 0; // this class's keys (a speed hint)
   }
@@ -651,10 +673,10 @@ CallPlan make_call_plan(const mvr_paged_attention_args* a) {
   p1.seq_lens_host = nullptr;
   p1.cu_q_lens_host = nullptr;
   LiveSeqs live1;
+  live1.count = count[1];
+  live1.split_count = last[1] - first[1] + 1;
   if (hinted) {
-    live1.count = count[1];
     if (sl) live1.max_seq_len = lmax[1];
-    live1.split_count = last[1] - first[1] + 1;
     p1.sum_seq_lens = sl ? lsum[1] : 0;
   }
   c.plan[1] = make_plan(&p1, true, live1, /*force_prefill=*/true);
@@ -997,6 +1019,9 @@ static int checked_attention_tables(const mvr_paged_attention_args* a) {
       if (a->cu_q_lens_host[s] != cu[s])
         return fail(MVR_E_INVALID_ARGUMENT, "cu_q_lens_host[%d] = %d differs from the device cu_q_lens (%d)", s,
                     a->cu_q_lens_host[s], cu[s]);
+  if (a->total_q > 0 && !cu.empty() && cu[a->num_seqs] > a->total_q)
+    return fail(MVR_E_INVALID_ARGUMENT, "the device cu_q_lens[num_seqs] = %d exceeds total_q = %d", cu[a->num_seqs],
+                a->total_q);
   return mvr_paged_attention_validate(a, ptr_or_null(bt), ptr_or_null(sl), ptr_or_null(cu));
 }
 
@@ -1198,6 +1223,9 @@ int mvr_paged_attention_validate(const mvr_paged_attention_args* a, const int32_
   g_last_error[0] = 0;
   int rc = check_scalars(a);
   if (rc != MVR_OK) return rc;
+  if (cu_q_lens_host && a->total_q > 0 && cu_q_lens_host[a->num_seqs] > a->total_q)
+    return fail(MVR_E_INVALID_ARGUMENT, "cu_q_lens[num_seqs] = %d exceeds total_q = %d", cu_q_lens_host[a->num_seqs],
+                a->total_q);
   for (int s = 0; s < a->num_seqs; s++) {
     const int seq_len = seq_lens_host ? seq_lens_host[s] : (a->num_seqs == 1 ? a->max_seq_len : -1);
     int q_len = -1;
@@ -1257,6 +1285,7 @@ static int layout_to_args(int32_t dtype, const mvr_attention_dimensions* dims, c
   a->num_pages = layout->page_count;
   a->max_pages_per_seq = layout->num_page_ids;
   a->max_q_len = dims->q_len;
+  a->total_q = dims->q_len;
   a->max_seq_len = layout->cached_token_count;
   a->q = request_q; // [1, Hq, q_len, D]
   a->q_stride_head = (int64_t)dims->q_len * dims->head_dim;

@@ -29,7 +29,7 @@ from typing import Optional, Sequence
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libmvr_attn.so")
 
-ABI_VERSION = 2  # MVR_ATTN_ABI_VERSION of include/mvr_attn.h
+ABI_VERSION = 3  # MVR_ATTN_ABI_VERSION of include/mvr_attn.h
 
 DTYPE_F32, DTYPE_F16 = 0, 1
 
@@ -102,6 +102,7 @@ class PagedAttentionArgs(ctypes.Structure):
         ("sum_seq_lens", ctypes.c_int64),
         ("seq_lens_host", ctypes.c_void_p),
         ("cu_q_lens_host", ctypes.c_void_p),
+        ("total_q", ctypes.c_int32),
     ]
 
 
@@ -324,6 +325,7 @@ def make_args(q, key_pool, value_pool, block_tables, seq_lens, cu_q_lens, out, *
     a.out_stride_token = out.stride(1)
     a.stream = _stream_handle(stream)
     a.sum_seq_lens = int(sum_seq_lens)
+    a.total_q = q.shape[1]
     sl_h, cu_h = _host_int32(seq_lens_host), _host_int32(cu_q_lens_host)
     if sl_h is not None and sl_h.shape != (a.num_seqs,):
         raise MvrError(MVR_E_INVALID_ARGUMENT, "seq_lens_host must hold num_seqs entries")

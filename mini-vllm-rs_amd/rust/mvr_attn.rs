@@ -16,7 +16,7 @@
 
 use std::ffi::{c_char, c_int, c_void, CStr};
 
-pub const MVR_ATTN_ABI_VERSION: c_int = 2;
+pub const MVR_ATTN_ABI_VERSION: c_int = 3;
 pub const MVR_NOALLOC_SCRATCH_BYTES: usize = 64 << 20;
 
 // ActivationDType (src/model_runner/mod.rs:331-351).
@@ -67,6 +67,7 @@ pub struct MvrPagedAttentionArgs {
     pub sum_seq_lens: i64,        // optional hint: sum of seq_lens (0 = unknown)
     pub seq_lens_host: *const i32, // optional hint: host copy of seq_lens (null = unknown)
     pub cu_q_lens_host: *const i32, // optional hint: host copy of cu_q_lens (null = unknown)
+    pub total_q: i32,               // token dimension of q and out (0 = unknown): bounds cu_q_lens[num_seqs]
 }
 
 #[repr(C)]

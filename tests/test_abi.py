@@ -30,7 +30,7 @@ def test_library_exports_every_declared_symbol():
     out = subprocess.run(["nm", "-D", "--defined-only", M.library_path()], capture_output=True, text=True, check=True)
     exported = set(re.findall(r"\bT (mvr_[a-z0-9_]+)$", out.stdout, flags=re.M))
     assert set(declared) <= exported
-    assert M.load_library().mvr_abi_version() == M.ABI_VERSION == 2
+    assert M.load_library().mvr_abi_version() == M.ABI_VERSION == 3
 
 
 def test_product_library_does_not_link_the_oracle():
@@ -80,6 +80,9 @@ def _call(a):
     ("q", 1 + (1 << 20), M.MVR_E_INVALID_ARGUMENT, "aligned"),
     ("q_stride_token", 100, M.MVR_E_INVALID_ARGUMENT, "aligned"),
     ("seq_lens", None, M.MVR_E_INVALID_ARGUMENT, "required"),
+    ("total_q", 1, M.MVR_E_INVALID_ARGUMENT, "total_q 1 is outside"),  # fewer tokens than sequences
+    ("total_q", 3, M.MVR_E_INVALID_ARGUMENT, "total_q 3 is outside"),  # more than num_seqs * max_q_len
+    ("total_q", -1, M.MVR_E_INVALID_ARGUMENT, "total_q -1 is outside"),
 ])
 def test_scalar_checks_reject_before_launch(field, value, code, msg):
     rc, err = _call(_args(**{field: value}))
@@ -200,6 +203,45 @@ def test_validate_mirrors_reference_errors():
         M.validate(a, bt, [1024, 17], [0, 0, 1])
     with pytest.raises(M.MvrError, match="max_seq_len"):
         M.validate(a, bt, [2000, 17], [0, 1, 2])
+    # q and out hold total_q tokens: the packed count may not exceed it
+    with pytest.raises(M.MvrError, match="exceeds total_q = 3"):
+        M.validate(_args(max_q_len=2, total_q=3), bt, [1024, 17], [0, 2, 4])
+    M.validate(_args(max_q_len=2, total_q=4), bt, [1024, 17], [0, 2, 4])
+    with pytest.raises(M.MvrError, match="smaller than max_q_len"):
+        M.validate(_args(num_seqs=1, max_q_len=5, total_q=4, cu_q_lens=None), bt, [1024], None)
+
+
+def _mixed_args(q_lens, seq_lens, hints, **kw):
+    """Scalar-only args (never launched) of a Llama-3-8B-shaped F16 call with these requests."""
+    import numpy as np
+    q_lens, seq_lens = np.asarray(q_lens, np.int32), np.asarray(seq_lens, np.int32)
+    cu = np.concatenate([[0], np.cumsum(q_lens)]).astype(np.int32)
+    kw.setdefault("total_q", int(cu[-1]))
+    a = _args(num_seqs=len(q_lens), max_q_len=int(q_lens.max()), max_seq_len=int(seq_lens.max()),
+              max_pages_per_seq=int(seq_lens.max() + 15) // 16, num_pages=1 << 16, sum_seq_lens=int(seq_lens.sum()),
+              **kw)
+    if hints:
+        a.seq_lens_host = seq_lens.ctypes.data
+        a.cu_q_lens_host = cu.ctypes.data
+    a._keep = (seq_lens, cu)
+    return a
+
+
+def test_mixed_batch_without_host_tables_plans_like_the_hinted_call():
+    # A scheduler step (decodes first, then the prefill chunks, scheduler.rs:258-271) without host copies of the
+    # length tables: total_q says how many prefill-sized requests the tail holds, so the plans (and the
+    # workspace they need) match the hinted call's.
+    step = dict(q_lens=[1] * 63 + [256], seq_lens=[8192] * 63 + [2304])
+    assert M.workspace_size(_mixed_args(**step, hints=False)) == M.workspace_size(_mixed_args(**step, hints=True))
+    two = dict(q_lens=[1] * 30 + [200, 200], seq_lens=[4096] * 30 + [1000, 3000])
+    assert M.workspace_size(_mixed_args(**two, hints=False)) == M.workspace_size(_mixed_args(**two, hints=True))
+    # A call whose tokens could fill every sequence with a prefill chunk runs as one prefill launch, as with
+    # hints that show one class; with total_q unknown it keeps the two launches (launch 0 over the decode
+    # shape: its own partial slots).
+    chunks = dict(q_lens=[256] * 4, seq_lens=[2304] * 4)
+    one = M.workspace_size(_mixed_args(**chunks, hints=True))
+    assert M.workspace_size(_mixed_args(**chunks, hints=False)) == one
+    assert M.workspace_size(_mixed_args(**chunks, hints=False, total_q=0)) != one
 
 
 def test_request_level_entry_checks_lengths():

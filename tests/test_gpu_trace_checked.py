@@ -155,6 +155,19 @@ def _checked_child(out_path):
             results[key] = (0, "")
         except M.MvrError as e:
             results[key] = (e.code, e.message)
+    # a device cu_q_lens packing one token more than q holds (the last request's q_len 2): q is a view one token
+    # short of the tensor it views and out is full-size, so every address the kernel could touch lies in
+    # allocated memory, should the check miss
+    q_big = torch.zeros((t["q"].shape[0], w.total_q + 1, t["q"].shape[2]), dtype=t["q"].dtype, device="cuda")
+    out_big = torch.empty_like(q_big)
+    cu_more = t["cu_q_lens"].clone()
+    cu_more[-1] += 1
+    try:
+        M.paged_attention(q_big[:, :w.total_q], t["key_pool"], t["value_pool"], t["block_tables"], t["seq_lens"],
+                          cu_more, out_big, max_q_len=2, max_seq_len=w.max_seq_len)
+        results["short_q"] = (0, "")
+    except M.MvrError as e:
+        results["short_q"] = (e.code, e.message)
     # rope + append writing a page outside the pool
     cos, sin = W.rope_tables(64, 10000.0, w.max_seq_len)
     q = t["q"]
@@ -238,6 +251,7 @@ def test_checked_mode_reports_broken_tables_and_runs_valid_calls():
             c["stale_seq_lens_msg"][0])
         assert int(c["stale_cu_q_lens"][0]) == M.MVR_E_INVALID_ARGUMENT and "cu_q_lens_host" in str(
             c["stale_cu_q_lens_msg"][0])
+        assert int(c["short_q"][0]) == M.MVR_E_INVALID_ARGUMENT and "exceeds total_q" in str(c["short_q_msg"][0])
         assert int(c["rope_page"][0]) == M.MVR_E_PAGE_ID
         assert int(c["cascade_page"][0]) == M.MVR_E_INVALID_ARGUMENT and "differs" in str(c["cascade_page_msg"][0])
 
