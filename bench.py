@@ -318,6 +318,32 @@ def measure_mixed(W, M, torch, steps, warmup):
     return res
 
 
+DECODE_MAP = [(4, 2048), (16, 2048), (64, 2048), (16, 8192), (32, 4096), (64, 8192), (128, 2048), (128, 8192)]
+
+
+def measure_decode_map(W, M, torch, steps, warmup):
+    """Ragged against uniform decode at about equal bytes (Llama-3-8B shape, F16): for each (batch, ctx), the
+    batch at ctx tokens each and the batch with lengths U[ctx/4, 7 ctx/4]; GB/s on each batch's own bytes."""
+    rows = []
+    for batch, ctx in DECODE_MAP:
+        row = dict(batch=batch, ctx=ctx)
+        for ragged in (False, True):
+            w = W.llama3_8b_decode_map_f16(batch, ctx, ragged)
+            t = W.device_tensors(w, None)
+            _, per = time_steps(Runner(w, t, torch, M, host_hints=True), torch, steps, warmup)
+            med = per[len(per) // 2]
+            key = "ragged" if ragged else "uniform"
+            row[key + "_us"] = round(med, 2)
+            row[key + "_gbs"] = round(w.algorithmic_bytes() / (med * 1e-6) / 1e9, 1)
+            del t
+            torch.cuda.empty_cache()
+        row["ragged_over_uniform"] = round(row["ragged_gbs"] / row["uniform_gbs"], 3)
+        log(f"[bench] decode map b{batch} ctx{ctx}: uniform {row['uniform_gbs']} GB/s, ragged {row['ragged_gbs']} "
+            f"GB/s ({row['ragged_over_uniform']:.0%})")
+        rows.append(row)
+    return rows
+
+
 def measure_append(W, M, torch, cfg, steps, warmup):
     w = W.CONFIGS[cfg]()
     t = W.device_tensors(w, None)
@@ -344,6 +370,8 @@ def main():
     ap.add_argument("--only-config", type=int, default=0, choices=(0, 1, 2, 4, 5),
                     help="time only this one of the other workloads and print its result (for profiling one kernel)")
     ap.add_argument("--only-mixed", action="store_true", help="time only the mixed decode + prefill batch")
+    ap.add_argument("--decode-map", action="store_true",
+                    help="time only ragged against uniform decode batches of about equal bytes (Llama-3-8B, F16)")
     ap.add_argument("--f32", action="store_true", help="with --only-config 4: the same chunked prefill in F32")
     a = ap.parse_args()
     if a.gpus != 1:
@@ -363,6 +391,9 @@ def main():
     M.load_library()
     if a.only_mixed:
         print(json.dumps({"mixed": measure_mixed(W, M, torch, a.steps, a.warmup)}), flush=True)
+        return
+    if a.decode_map:
+        print(json.dumps({"decode_map": measure_decode_map(W, M, torch, a.steps, a.warmup)}), flush=True)
         return
     if a.f32 and a.only_config != 4:
         print("--f32 goes with --only-config 4", file=sys.stderr)

@@ -195,8 +195,10 @@ mvr::PagedAttentionPlan make_plan(const mvr_paged_attention_args* a, bool allow_
   // LDS-shared 32x32 MFMA kernel (F16 32x32x16, F32 32x32x2).
   // MVR_ATTN_PREFILL_KERNEL=false keeps every call on the split-context kernel.
   static const bool prefill_enabled = env_bool("MVR_ATTN_PREFILL_KERNEL", true);
-  const bool page_pow2 = (a->page_size & (a->page_size - 1)) == 0;
-  if (allow_prefill && prefill_enabled && (rows_max > 64 || force_prefill) && page_pow2) {
+  // (Its loads take 16-token runs, 8 in F32, inside one page: page sizes
+  // that are multiples of 16, as every size is after the repack.)
+  const bool page_runs = a->page_size % mvr::kChunkTokens == 0;
+  if (allow_prefill && prefill_enabled && (rows_max > 64 || force_prefill) && page_runs) {
     plan.prefill = true;
     plan.row_tiles = (int)((rows_max + mvr::kPrefillBlockRows - 1) / mvr::kPrefillBlockRows);
     const int64_t live_blocks = n_live * a->num_kv_heads * plan.row_tiles;
@@ -480,8 +482,7 @@ int launch_planned(const mvr_paged_attention_args* a, const mvr::PagedAttentionP
     f.num_kv_heads = a->num_kv_heads;
     f.group_size = a->num_q_heads / a->num_kv_heads;
     f.page_size = a->page_size;
-    f.page_shift = 0;
-    while ((1 << f.page_shift) < a->page_size) f.page_shift++; // page_size is a power of two here
+    mvr::page_divider(a->page_size, f.page_magic, f.page_magic_shift);
     f.row_tiles = plan.row_tiles;
     f.kv_splits = plan.kv_splits;
     f.scale_log2 = scale * 1.4426950408889634f;
@@ -596,8 +597,7 @@ CallPlan make_call_plan(const mvr_paged_attention_args* a) {
   const int group = a->num_q_heads / a->num_kv_heads;
   const int small_q = kSmallRows / group; // largest q_len of the small class (0: no such class)
   if (a->num_seqs < 2 || small_q < 1 || a->max_q_len <= small_q) return c;
-  const bool page_pow2 = (a->page_size & (a->page_size - 1)) == 0;
-  if (!c.plan[0].prefill || !page_pow2) return c; // launch 1 needs the prefill kernel
+  if (!c.plan[0].prefill) return c; // launch 1 needs the prefill kernel
   const int32_t* cu = a->cu_q_lens_host;
   const int32_t* sl = a->seq_lens_host;
   int first[2] = {-1, -1}, last[2] = {-1, -1}, count[2] = {0, 0}, lmax[2] = {0, 0}, qmax = 0;

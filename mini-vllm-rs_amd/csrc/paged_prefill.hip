@@ -245,11 +245,11 @@ __device__ __forceinline__ void prefill_tile_serial(const PrefillParams& p, cons
   // index, so they are scalar loads and never wait on the K/V loads in flight.
   const const_i32* bt = (const const_i32*)(p.block_tables) + (int64_t)b * p.block_table_stride;
 
-  // Page arithmetic by shifts: the host routes only power-of-two page sizes
-  // (multiples of 16) to this kernel.
-  const int pshift = p.page_shift;
-  auto page_div = [&](int tok) { return tok >> pshift; };
-  auto page_mod = [&](int tok) { return tok & (p.page_size - 1); };
+  // Page arithmetic by a multiply and a shift (wave-uniform: scalar
+  // instructions once per step); the host routes page sizes that are
+  // multiples of 16 to this kernel.
+  auto page_div = [&](int tok) { return (int)(((uint64_t)(uint32_t)tok * p.page_magic) >> p.page_magic_shift); };
+  auto page_mod = [&](int tok) { return tok - page_div(tok) * p.page_size; };
 
   // A stage holds the 2 TT tokens of one step: tile j0 + 2i (group 0) in rows
   // 0..TT-1 and tile j0 + 2i + 1 (group 1) in rows TT..2TT-1.  Tokens move
@@ -261,7 +261,7 @@ __device__ __forceinline__ void prefill_tile_serial(const PrefillParams& p, cons
   // holds token row t = P / (D/8), physical chunk P % (D/8), and the lane
   // fetches the logical 16-byte chunk that the K or V swizzle puts there.  A
   // wavefront's R tokens are consecutive and start at a multiple of R, hence
-  // lie in one page (page sizes here are powers of two, at least 16): one
+  // lie in one page (page sizes here are multiples of 16): one
   // scalar block-table load, one page address and one bound per wavefront
   // and step.  That page row goes into the buffer base, so a lane's byte
   // offset within the wavefront's tokens never changes and the loop spends no

@@ -23,8 +23,11 @@ struct PrefillParams {
   int64_t out_stride_head, out_stride_token;
   float* partial_o;  // [slots][128][head_dim] fp32 when kv_splits > 1
   float* partial_ml; // [slots][128][2]
-  int32_t num_seqs, num_kv_heads, group_size, page_size;
-  int32_t page_shift; // log2(page_size); page_size is a power of two
+  int32_t num_seqs, num_kv_heads, group_size, page_size; // page_size: a multiple of 16
+  // Page of a token without a divide: page = tok * page_magic >> page_magic_shift
+  // for every tok in [0, 2^31) (page_divider).
+  uint64_t page_magic;
+  int32_t page_magic_shift;
   int32_t row_tiles;  // 128-row tiles per (sequence, kv head)
   int32_t kv_splits; // key-range splits per row tile
   float scale_log2;
@@ -48,6 +51,19 @@ struct PrefillParams {
   // cover sequences that host hints placed in another launch's class).
   int32_t catch_lo, catch_count;
 };
+
+// Division by the invariant page_size as a multiply and a shift, the
+// round-up method of Granlund and Montgomery ("Division by invariant integers
+// using multiplication", PLDI 1994, theorem 4.2): with l = ceil(log2 d),
+// shift = 32 + l and magic = ceil(2^shift / d), 2^shift <= magic * d <=
+// 2^shift + 2^l, so floor(n * magic / 2^shift) = floor(n / d) for every n <
+// 2^32; magic < 2^33 + 1 keeps n * magic below 2^64 for n < 2^31.
+inline void page_divider(int32_t d, uint64_t& magic, int32_t& shift) {
+  int l = 0;
+  while ((1ll << l) < d) l++;
+  shift = 32 + l;
+  magic = (uint64_t)((((unsigned __int128)1 << shift) + (unsigned)d - 1) / (unsigned)d);
+}
 
 // f32: F32 Q/K/V/out (v_mfma_f32_32x32x2_f32); otherwise F16.
 hipError_t launch_paged_prefill(const PrefillParams& params, int head_dim, bool f32, hipStream_t stream);

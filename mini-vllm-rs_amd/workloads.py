@@ -189,6 +189,23 @@ def llama3_8b_mixed_decode_prefill_f16(num_decode: int = 63, decode_ctx: int = 8
                     32, 8, 128, 16, num_pages, 0.3, seq_lens, q_lens, bt, seed)
 
 
+def llama3_8b_decode_map_f16(batch: int, ctx: int, ragged: bool) -> Workload:
+    """Llama-3-8B-shaped F16 decode (32 Q / 8 KV, D 128, one query token each) over `batch` sequences of `ctx`
+    cached tokens (uniform) or of lengths drawn from U[ctx/4, 7 ctx/4] (ragged: the same mean, so about the same
+    bytes), 16-token pages in random order, pool = exact fit."""
+    seed = SEED_BASE + 11 + batch + ctx + int(ragged)
+    rng = np.random.default_rng(seed)
+    if ragged:
+        seq_lens = rng.integers(ctx // 4, 7 * ctx // 4, size=batch, endpoint=True).astype(np.int32)
+    else:
+        seq_lens = np.full(batch, ctx, np.int32)
+    num_pages = int(sum(math.ceil(int(L) / 16) for L in seq_lens))
+    bt = _assign_pages(rng, seq_lens, 16, num_pages)
+    kind = f"U[{ctx // 4},{7 * ctx // 4}]" if ragged else f"{ctx}"
+    return Workload(f"llama3-8b decode f16 b{batch} ctx{kind}", "f16", 32, 8, 128, 16, num_pages, 0.3, seq_lens,
+                    np.ones(batch, np.int32), bt, seed)
+
+
 def llama3_8b_spec_verify_f16() -> Workload:
     """16 sequences verifying 5 positions; contexts U[1024, 16384]; groups of 4 share the first 1024 tokens' pages."""
     seed = SEED_BASE + 5

@@ -489,6 +489,35 @@ def test_page_sizes_off_16_match_oracle_and_16_token_pages(page_size, dtype, hq,
     assert err <= (2e-3 if dtype == "f16" else 1e-5) and diff == 0
 
 
+@pytest.mark.parametrize("page_size", [48, 80, 272])
+@pytest.mark.parametrize("dtype,hq,hkv,d", [("f16", 28, 4, 128), ("f32", 14, 2, 64)])
+def test_prefill_page_sizes_multiple_of_16_match_oracle_and_16_token_pages(page_size, dtype, hq, hkv, d):
+    # Page sizes that are multiples of 16 but not powers of two run the chunked-prefill kernel in place (its
+    # page arithmetic is a multiply and a shift): chunks with and without a cached prefix, a page boundary
+    # inside most 8-token load runs' neighbourhoods, and a decode row; bit for bit the 16-token-page result.
+    q_lens = [200, 64, 130, 1]
+    seq_lens = [700, 64, 130 + 5 * page_size + 24, 333]
+    q, layouts = _same_tokens_two_page_sizes(700 + page_size, dtype, hq, hkv, d, seq_lens, q_lens, page_size)
+    outs = []
+    for P, kp, vp, bt in layouts:
+        out = M.paged_attention(torch.from_numpy(q).cuda(), torch.from_numpy(kp).cuda(), torch.from_numpy(vp).cuda(),
+                                torch.from_numpy(bt).cuda(), torch.tensor(seq_lens, dtype=torch.int32).cuda(),
+                                torch.tensor(np.concatenate([[0], np.cumsum(q_lens)]), dtype=torch.int32).cuda(),
+                                max_q_len=max(q_lens), max_seq_len=max(seq_lens), sum_seq_lens=int(sum(seq_lens)))
+        torch.cuda.synchronize()
+        outs.append(out.cpu().numpy())
+    P, kp, vp, bt = layouts[0]
+    ref = O.paged_attention(q, kp, vp, bt, np.asarray(seq_lens, np.int32),
+                            np.concatenate([[0], np.cumsum(q_lens)]).astype(np.int32), hq, hkv, d, P,
+                            dtype=O.F16 if dtype == "f16" else O.F32, num_threads=16)
+    err = float(np.abs(outs[0].astype(np.float64) - ref).max())
+    view = np.uint16 if dtype == "f16" else np.uint32
+    diff = int(np.count_nonzero(outs[0].view(view) != outs[1].view(view)))
+    say(f"[prefill page size {page_size}] {dtype} D={d}: max-abs vs oracle {err:.3e}; "
+        f"{diff} outputs differ from 16-token pages")
+    assert np.isfinite(outs[0]).all() and err <= (2e-3 if dtype == "f16" else 1e-5) and diff == 0
+
+
 @pytest.mark.parametrize("page_size,seq_len,q_len", [(16, 8192, 1), (16, 1000, 1), (5, 700, 1), (16, 1000, 200)])
 def test_pages_past_2_pow_31_elements(page_size, seq_len, q_len):
     # Page ids above 2^31 / (Hkv * page_size * D) put their elements past 2^31 in the pool, so every offset must
