@@ -318,6 +318,18 @@ def measure_mixed(W, M, torch, steps, warmup):
     return res
 
 
+def measure_page_sizes(W, M, torch, steps, warmup):
+    """Configs 3 and 4 in pages of other sizes (README.md:175-176 lets the runner pick any): multiples of 16
+    are read in place, other sizes repacked into 16-token pages in the workspace first (a K/V copy inside every
+    call)."""
+    res = {}
+    for cfg, sizes in ((3, (32, 48, 8, 5)), (4, (48, 8))):
+        for ps in sizes:
+            log(f"[bench] config {cfg} in {ps}-token pages")
+            res[f"{cfg}/{ps}"] = measure(W, M, torch, lambda: W.repaged(W.CONFIGS[cfg](), ps), steps, warmup)
+    return res
+
+
 DECODE_MAP = [(4, 2048), (16, 2048), (64, 2048), (16, 8192), (32, 4096), (64, 8192), (128, 2048), (128, 8192)]
 
 
@@ -370,6 +382,7 @@ def main():
     ap.add_argument("--only-config", type=int, default=0, choices=(0, 1, 2, 4, 5),
                     help="time only this one of the other workloads and print its result (for profiling one kernel)")
     ap.add_argument("--only-mixed", action="store_true", help="time only the mixed decode + prefill batch")
+    ap.add_argument("--page-sizes", action="store_true", help="time only configs 3 and 4 in other page sizes")
     ap.add_argument("--decode-map", action="store_true",
                     help="time only ragged against uniform decode batches of about equal bytes (Llama-3-8B, F16)")
     ap.add_argument("--f32", action="store_true", help="with --only-config 4: the same chunked prefill in F32")
@@ -391,6 +404,9 @@ def main():
     M.load_library()
     if a.only_mixed:
         print(json.dumps({"mixed": measure_mixed(W, M, torch, a.steps, a.warmup)}), flush=True)
+        return
+    if a.page_sizes:
+        print(json.dumps({"page_sizes": measure_page_sizes(W, M, torch, a.steps, a.warmup)}), flush=True)
         return
     if a.decode_map:
         print(json.dumps({"decode_map": measure_decode_map(W, M, torch, a.steps, a.warmup)}), flush=True)
@@ -493,6 +509,7 @@ def main():
         log("[bench] shared-prompt decode, cascade and plain")
         result["cascade"]["shared_prompt"] = measure_cascade(W, M, torch, W.llama3_8b_shared_prompt_decode_f16,
                                                              max(20, a.steps // 2), a.warmup, with_plain=True)
+        result["page_sizes"] = measure_page_sizes(W, M, torch, max(20, a.steps // 2), a.warmup)
         result["rope_append"] = {}
         for cfg in (3, 4):
             log(f"[bench] rope+append, config {cfg}")

@@ -206,6 +206,16 @@ def llama3_8b_decode_map_f16(batch: int, ctx: int, ragged: bool) -> Workload:
                     np.ones(batch, np.int32), bt, seed)
 
 
+def repaged(w: Workload, page_size: int) -> Workload:
+    """The same requests (lengths, query lengths, heads, dtype) stored in pages of page_size tokens in a random
+    order, pool = exact fit: for timing a page size against the 16-token layout."""
+    rng = np.random.default_rng(w.seed + 1000 * page_size)
+    num_pages = int(sum(math.ceil(int(L) / page_size) for L in w.seq_lens))
+    bt = _assign_pages(rng, w.seq_lens, page_size, num_pages)
+    return Workload(f"{w.name}, {page_size}-token pages", w.dtype, w.num_q_heads, w.num_kv_heads, w.head_dim, page_size,
+                    num_pages, w.value_scale, w.seq_lens.copy(), w.q_lens.copy(), bt, w.seed)
+
+
 def llama3_8b_spec_verify_f16() -> Workload:
     """16 sequences verifying 5 positions; contexts U[1024, 16384]; groups of 4 share the first 1024 tokens' pages."""
     seed = SEED_BASE + 5
