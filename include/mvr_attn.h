@@ -81,8 +81,10 @@ typedef struct mvr_paged_attention_args {
   int32_t num_q_heads;
   int32_t num_kv_heads;      /* divides num_q_heads */
   int32_t head_dim;          /* 64 or 128 */
-  int32_t page_size;         /* per_page_token_count, any positive value; a size that is not a multiple
-                                of 16 is repacked into 16-token pages in the workspace first */
+  int32_t page_size;         /* per_page_token_count, any positive value; sizes that are not a multiple of
+                                16 are read in place by decode-sized calls (2 tokens or more), and
+                                repacked into 16-token pages in the workspace first by prefill-sized calls
+                                and for 1-token pages */
   int64_t num_pages;         /* page_count of each pool */
   int32_t max_pages_per_seq; /* row stride of block_tables */
   int32_t max_q_len;         /* >= every q_len (host-side bound, sizes the grid) */
@@ -147,8 +149,8 @@ int mvr_paged_attention(const mvr_paged_attention_args* args);
    over a workspace (code under HIP graph capture, tight serving loops,
    harnesses that forbid hipMalloc).  Same arguments, output and numerics as
    mvr_paged_attention, except that args->workspace and workspace_bytes are
-   ignored: the split-context partials (and the 16-token repack of page sizes
-   that are not a multiple of 16) live in a static device array of the
+   ignored: the split-context partials (and the 16-token repack of pages that
+   a call cannot read in place) live in a static device array of the
    library, MVR_NOALLOC_SCRATCH_BYTES per device, held from the first use on
    that device until the process ends.  A call that needs more returns
    MVR_E_WORKSPACE (use mvr_paged_attention with a workspace for it).  It

@@ -198,6 +198,9 @@ mvr::PagedAttentionPlan make_plan(const mvr_paged_attention_args* a, bool allow_
   // (Its loads take 16-token runs, 8 in F32, inside one page: page sizes
   // that are multiples of 16, as every size is after the repack.)
   const bool page_runs = a->page_size % mvr::kChunkTokens == 0;
+  // Other page sizes reach make_plan only for calls that the split-context
+  // kernel serves, which then reads them in place (token pages).
+  plan.token_pages = !page_runs;
   if (allow_prefill && prefill_enabled && (rows_max > 64 || force_prefill) && page_runs) {
     plan.prefill = true;
     plan.row_tiles = (int)((rows_max + mvr::kPrefillBlockRows - 1) / mvr::kPrefillBlockRows);
@@ -303,7 +306,7 @@ mvr::PagedAttentionPlan make_plan(const mvr_paged_attention_args* a, bool allow_
   // for head_dim 64 only.  MVR_ATTN_BLOCK_MERGE=false keeps the separate merge.
   static const bool block_merge_enabled = env_bool("MVR_ATTN_BLOCK_MERGE", true);
   plan.block_waves = 0;
-  if (block_merge_enabled && !ragged && plan.row_blocks == 1) {
+  if (block_merge_enabled && !ragged && plan.row_blocks == 1 && !plan.token_pages) {
     const int widest = a->dtype != MVR_DTYPE_F16 ? 4 : a->head_dim == 64 ? 16 : 8;
     for (int w = 4; w <= widest && plan.block_waves == 0; w *= 2)
       if (plan.max_parts <= w && 4 * plan.max_parts >= 3 * w) plan.block_waves = w;
@@ -329,7 +332,8 @@ mvr::PagedAttentionPlan make_plan(const mvr_paged_attention_args* a, bool allow_
   // turns it off.
   static const bool dense_enabled = env_bool("MVR_ATTN_DENSE_RAGGED", true);
   bool dense = false;
-  if (dense_enabled && ragged && plan.row_tiles == 1 && plan.max_parts > 1 && !plan.block_merge && n_live >= 32) {
+  if (dense_enabled && ragged && plan.row_tiles == 1 && plan.max_parts > 1 && !plan.block_merge && n_live >= 32 &&
+      !plan.token_pages) {
     const int64_t chunk_tokens = (int64_t)mvr::kChunkTokens * plan.chunks_per_part;
     const int64_t est_live = (a->sum_seq_lens + chunk_tokens - 1) / chunk_tokens + n_live / 2;
     dense = est_live * 10 < (int64_t)a->num_seqs * plan.max_parts * 7; // live fraction < 0.7
@@ -377,8 +381,8 @@ mvr::PagedAttentionPlan make_plan(const mvr_paged_attention_args* a, bool allow_
   // MVR_ATTN_DEEP_PIPELINE=false turns it off.
   static const bool deep_enabled = env_bool("MVR_ATTN_DEEP_PIPELINE", true);
   const int elem_bytes = a->dtype == MVR_DTYPE_F16 ? 2 : 4;
-  plan.deep_pipeline = deep_enabled && ragged && !dense && !plan.block_merge && plan.row_blocks == 1 &&
-                       a->head_dim * elem_bytes <= 256 && plan.chunks_per_part >= 8;
+  plan.deep_pipeline = deep_enabled && ragged && !dense && !plan.block_merge && !plan.token_pages &&
+                       plan.row_blocks == 1 && a->head_dim * elem_bytes <= 256 && plan.chunks_per_part >= 8;
   // No padding of max_parts.  Padding it to a multiple of 32 / gcd(Hkv * row
   // tiles, 32) made partition p of every sequence run on the same XCD (so
   // that pages shared by several sequences would meet in one L2), but the
@@ -415,6 +419,7 @@ mvr::PagedAttentionPlan make_plan(const mvr_paged_attention_args* a, bool allow_
     static const int unit_waves_override = env_int("MVR_ATTN_UNIT_WAVES", 0);
     if (unit_waves_override == 1 || unit_waves_override == 2 || unit_waves_override == 4)
       plan.unit_waves = unit_waves_override;
+    if (plan.token_pages) plan.unit_waves = 1; // its one instantiation
   }
   plan.partial_bytes = 0;
   if (plan.max_parts > 1 && !plan.block_merge) {
@@ -517,6 +522,7 @@ int launch_planned(const mvr_paged_attention_args* a, const mvr::PagedAttentionP
   p.cu_q_lens = a->cu_q_lens;
   p.single_seq_len = a->max_seq_len;
   p.single_q_len = a->max_q_len;
+  mvr::page_divider(a->page_size, p.page_magic, p.page_magic_shift);
   p.out = a->out;
   p.out_stride_head = a->out_stride_head;
   p.out_stride_token = a->out_stride_token;
@@ -721,6 +727,21 @@ struct RepackPlan {
   int pages16;
   size_t off_part, total;
 };
+
+// Page sizes that are not a multiple of 16 are read in place by the
+// split-context kernel (token pages) down to 2 tokens per page; a call that
+// would use the chunked-prefill kernel (whose loads need 16-token runs inside
+// a page) or pages of one token is repacked into 16-token pages first.
+bool needs_repack(const mvr_paged_attention_args* a) {
+  if (a->page_size % mvr::kChunkTokens == 0) return false;
+  if (a->page_size < 2) return true;
+  mvr_paged_attention_args b = *a;
+  b.page_size = mvr::kChunkTokens; // the plan the repacked call would take
+  const CallPlan c = make_call_plan(&b);
+  for (int k = 0; k < c.n; k++)
+    if (c.plan[k].prefill) return true;
+  return false;
+}
 
 RepackPlan make_repack_plan(const mvr_paged_attention_args* a, char* ws) {
   RepackPlan r;
@@ -995,7 +1016,7 @@ int mvr_rope_append_validate(const mvr_rope_append_args* a, const int32_t* block
 
 size_t mvr_paged_attention_workspace_size(const mvr_paged_attention_args* args) {
   if (check_scalars(args) != MVR_OK) return 0;
-  if (args->page_size % mvr::kChunkTokens != 0) return make_repack_plan(args, nullptr).total;
+  if (needs_repack(args)) return make_repack_plan(args, nullptr).total;
   return make_call_plan(args).total;
 }
 
@@ -1059,7 +1080,7 @@ static void* noalloc_scratch() {
 // arguments carry (scalar checks already done).
 static int paged_attention_launches(const mvr_paged_attention_args* a) {
   int rc;
-  if (a->page_size % mvr::kChunkTokens != 0) {
+  if (needs_repack(a)) {
     const RepackPlan r = make_repack_plan(a, static_cast<char*>(a->workspace));
     rc = check_workspace(a, r.total);
     if (rc != MVR_OK) return rc;
@@ -1093,7 +1114,7 @@ int mvr_paged_attention_noalloc(const mvr_paged_attention_args* a) {
   int rc = check_scalars(a);
   if (rc != MVR_OK) return rc;
   const size_t need =
-      a->page_size % mvr::kChunkTokens != 0 ? make_repack_plan(a, nullptr).total : make_call_plan(a).total;
+      needs_repack(a) ? make_repack_plan(a, nullptr).total : make_call_plan(a).total;
   if (need > (size_t)MVR_NOALLOC_SCRATCH_BYTES)
     return fail(MVR_E_WORKSPACE,
                 "this call needs %zu bytes of scratch, more than the %zu bytes of the library's static scratch; "

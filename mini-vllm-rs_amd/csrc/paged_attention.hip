@@ -234,6 +234,19 @@ struct F16Traits {
     }
   }
 
+  // Pages that do not hold whole 16-token chunks: the same loads through a
+  // pointer to each token row (K: the lane's row is l & 15; V: load u reads
+  // token row v_row(l, u) at column v_col(l, u)).
+  __device__ static __forceinline__ void load_k_row(const half_t* row, int l, kreg_t (&k)[kLoads]) {
+#pragma unroll
+    for (int s = 0; s < kLoads; s++) k[s] = *reinterpret_cast<const half8*>(row + 8 * (l >> 4) + 32 * s);
+  }
+  __device__ static __forceinline__ int v_row(int l, int u) { return (l + 64 * u) / (D / 8); }
+  __device__ static __forceinline__ int v_col(int l, int u) { return 8 * ((l + 64 * u) % (D / 8)); }
+  __device__ static __forceinline__ vreg_t load_v_row(const half_t* row, int l, int u) {
+    return *reinterpret_cast<const half8*>(row + v_col(l, u));
+  }
+
   __device__ static __forceinline__ void stage_v(half_t* lds, int l, int tok_valid, const vreg_t (&v)[kLoads]) {
 #pragma unroll
     for (int u = 0; u < kLoads; u++) {
@@ -312,6 +325,16 @@ struct F32Traits {
     for (int u = 0; u < kLoads; u++) v[u] = *reinterpret_cast<const float4v*>(slab + 4 * (l + 64 * u));
   }
 
+  __device__ static __forceinline__ void load_k_row(const float* row, int l, kreg_t (&k)[kLoads]) {
+#pragma unroll
+    for (int u = 0; u < kLoads; u++) k[u] = *reinterpret_cast<const float4v*>(row + 4 * (l >> 4) + 16 * u);
+  }
+  __device__ static __forceinline__ int v_row(int l, int u) { return (l + 64 * u) / (D / 4); }
+  __device__ static __forceinline__ int v_col(int l, int u) { return 4 * ((l + 64 * u) % (D / 4)); }
+  __device__ static __forceinline__ vreg_t load_v_row(const float* row, int l, int u) {
+    return *reinterpret_cast<const float4v*>(row + v_col(l, u));
+  }
+
   __device__ static __forceinline__ void stage_v(float* lds, int l, int tok_valid, const vreg_t (&v)[kLoads]) {
 #pragma unroll
     for (int u = 0; u < kLoads; u++) {
@@ -376,12 +399,17 @@ struct F32Traits {
 // Block shape of a variant: WPB wavefronts; 16-wavefront blocks (4 per SIMD)
 // leave 128 VGPRs per lane.  Blocks of 1, 2 or 4 wavefronts without block
 // merge compile to the same registers per wavefront.
+// Token pages: block-table entries a 16-token chunk can touch when pages
+// hold P >= 2 tokens (ceil(15 / P) + 1).
+constexpr int kTpWindow = 9;
+
 template <typename Tr, int NB, int DEPTH, int WPB>
 constexpr int kernel_min_blocks() {
   return WPB > kWavesPerBlock ? 1 : (DEPTH == 3 ? 2 : Tr::template min_blocks<NB>());
 }
 
-template <typename Tr, int D, int NB, bool BM = false, bool DENSE = false, int DEPTH = 2, int WPB = kWavesPerBlock>
+template <typename Tr, int D, int NB, bool BM = false, bool DENSE = false, int DEPTH = 2, int WPB = kWavesPerBlock,
+          bool TP = false>
 __global__ __launch_bounds__(kWaveSize* WPB, (kernel_min_blocks<Tr, NB, DEPTH, WPB>())) void
     paged_attention_kernel(PagedAttentionParams p) {
   typedef typename Tr::elem T;
@@ -538,9 +566,49 @@ __global__ __launch_bounds__(kWaveSize* WPB, (kernel_min_blocks<Tr, NB, DEPTH, W
   };
 
   auto load_chunk = [&](int k, typename Tr::kreg_t (&kr)[Tr::kLoads], typename Tr::vreg_t (&vr)[Tr::kLoads]) {
-    const int64_t off = slab_offset(k);
-    Tr::load_k(kpool + off, l, kr);
-    Tr::load_v(vpool + off, l, vr);
+    if constexpr (TP) {
+      // Token pages (TP): page sizes that are not a multiple of 16, at least
+      // 2, read in place.  Token t lies in page t / P (a multiply and a
+      // shift) at slot t mod P; the chunk's tokens lie in at most
+      // ceil(15 / P) + 1 <= kTpWindow consecutive block-table entries, read
+      // as scalars, and each lane picks its row's page from them.  Rows past
+      // the call's last key read the last key's row (masked, and zeroed in
+      // the V stage), so every address lies in a page of the sequence.
+      const int tok0 = k * kChunkTokens;
+      const int tmax = s.key_end - 1; // >= tok0: chunk k holds a key
+      auto pdiv = [&](int t) { return (int)(((uint64_t)(uint32_t)t * p.page_magic) >> p.page_magic_shift); };
+      const int pf = pdiv(tok0);
+      const int pl = pdiv(min(tok0 + kChunkTokens - 1, tmax));
+      // Row r's element offset in the pools: (page * Hkv + h) * P + slot, times D.
+      int64_t roff[1 + Tr::kLoads];
+#pragma unroll
+      for (int i = 0; i <= Tr::kLoads; i++) {
+        const int r = i == 0 ? (l & 15) : Tr::v_row(l, i - 1);
+        const int t = min(tok0 + r, tmax);
+        const int pi = pdiv(t);
+        roff[i] = t - pi * p.page_size; // slot
+      }
+      int64_t pg[1 + Tr::kLoads];
+#pragma unroll
+      for (int i = 0; i <= Tr::kLoads; i++) pg[i] = 0;
+#pragma unroll
+      for (int j = 0; j < kTpWindow; j++) {
+        const int page = __builtin_amdgcn_readfirstlane(bt[min(pf + j, pl)]);
+#pragma unroll
+        for (int i = 0; i <= Tr::kLoads; i++) {
+          const int r = i == 0 ? (l & 15) : Tr::v_row(l, i - 1);
+          pg[i] = pdiv(min(tok0 + r, tmax)) - pf == j ? page : pg[i];
+        }
+      }
+      Tr::load_k_row(kpool + ((pg[0] * p.num_kv_heads + h) * p.page_size + roff[0]) * D, l, kr);
+#pragma unroll
+      for (int u = 0; u < Tr::kLoads; u++)
+        vr[u] = Tr::load_v_row(vpool + ((pg[1 + u] * p.num_kv_heads + h) * p.page_size + roff[1 + u]) * D, l, u);
+    } else {
+      const int64_t off = slab_offset(k);
+      Tr::load_k(kpool + off, l, kr);
+      Tr::load_v(vpool + off, l, vr);
+    }
   };
 
   // DEPTH chunks in flight; a tail past k1 reloads chunk k1 - 1 (an L2 hit)
@@ -858,7 +926,12 @@ __global__ __launch_bounds__(256) void merge_partitions_kernel(PagedAttentionPar
 template <typename Tr, int D, int NB, int WPB>
 hipError_t launch_units(const PagedAttentionPlan& plan, const PagedAttentionParams& params, hipStream_t stream) {
   const int64_t blocks = (plan.num_units + WPB - 1) / WPB;
-  if (plan.dense_parts) {
+  if (plan.token_pages) {
+    // planned with one wavefront per block, two chunks in flight, slot == partition
+    if (WPB != 1 || plan.dense_parts || plan.deep_pipeline) return hipErrorInvalidValue;
+    hipLaunchKernelGGL((paged_attention_kernel<Tr, D, NB, false, false, 2, 1, true>), dim3((unsigned)blocks),
+                       dim3(kWaveSize), 0, stream, params);
+  } else if (plan.dense_parts) {
     if (params.row_tiles != 1) return hipErrorInvalidValue; // dense_unit walks row tile 0 only
     hipLaunchKernelGGL((paged_attention_kernel<Tr, D, NB, false, true, 2, WPB>), dim3((unsigned)blocks),
                        dim3(kWaveSize * WPB), 0, stream, params);

@@ -54,6 +54,10 @@ struct PagedAttentionParams {
   // a batch mixing decode-sized and prefill-sized requests runs each class
   // on a grid planned for it.
   int32_t class_q_min, class_q_max;
+  // Token pages (page sizes that are not a multiple of 16): page of token t =
+  // t * page_magic >> page_magic_shift (mvr::page_divider).
+  uint64_t page_magic;
+  int32_t page_magic_shift;
 };
 
 // Grid shape chosen by the host.
@@ -73,6 +77,7 @@ struct PagedAttentionPlan {
   bool dense_parts;     // ragged split plan: live units first, in a dense order (see dense_unit)
   bool deep_pipeline;   // three chunks in flight per wavefront instead of two (16-row tiles only)
   int unit_waves;       // split plans without block merge: wavefronts per block, 1, 2 or 4 (0 means 4)
+  bool token_pages;     // pages that do not hold whole 16-token chunks, read in place (page_size >= 2)
 };
 
 hipError_t launch_paged_attention(const PagedAttentionPlan& plan, PagedAttentionParams params, hipStream_t stream);

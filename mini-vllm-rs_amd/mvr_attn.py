@@ -344,8 +344,8 @@ def workspace_size(args: PagedAttentionArgs) -> int:
 
 
 def new_workspace(nbytes: int, device):
-    """Device scratch for context-partition partials, and for the 16-token repack of pages whose size is not a
-    multiple of 16 (no initialisation needed)."""
+    """Device scratch for context-partition partials, and for the 16-token repack of pages that a call cannot
+    read in place (no initialisation needed)."""
     return _torch().empty(max(int(nbytes), 256), dtype=_torch().uint8, device=device)
 
 

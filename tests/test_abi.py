@@ -133,19 +133,25 @@ def test_workspace_too_small_is_rejected():
     assert rc == M.MVR_E_WORKSPACE and "smaller than" in err
 
 
-def test_page_sizes_off_16_are_repacked_in_the_workspace():
-    # A page size that is not a multiple of 16 (the reference's own tests use 2 and 3) is accepted: the call
-    # repacks each sequence's tokens into 16-token pages in the workspace, then runs the plan of that layout.
-    a16 = _args(max_seq_len=1024)
-    p16 = M.workspace_size(a16)
-    a3 = _args(max_seq_len=1024, page_size=3, max_pages_per_seq=342)
-    need = M.workspace_size(a3)
+def test_page_sizes_off_16_in_place_or_repacked():
+    # Any page size is accepted (the reference's own tests use 2 and 3).  Decode-sized calls read pages of 2 or
+    # more tokens in place: the workspace holds only their partials, as with 16-token pages.  Calls that take
+    # the chunked-prefill kernel, and pages of one token, repack each sequence's tokens into 16-token pages in
+    # the workspace first, then run the plan of that layout.
     pool = 2 * 64 * 8 * 16 * 128 * 2  # sequences x pages16 x kv heads x 16 tokens x head_dim x f16
+    p16 = M.workspace_size(_args(max_seq_len=1024))
+    assert M.workspace_size(_args(max_seq_len=1024, page_size=3, max_pages_per_seq=342)) == p16
+    assert M.workspace_size(_args(max_seq_len=1024, page_size=40, max_pages_per_seq=26)) == p16
+    a1 = _args(max_seq_len=1024, page_size=1, max_pages_per_seq=1024)
+    need = M.workspace_size(a1)
     assert need >= 2 * pool + 2 * 64 * 4 + p16
-    a3.workspace = 1 << 20
-    a3.workspace_bytes = need - 1
-    rc, err = _call(a3)
+    a1.workspace = 1 << 20
+    a1.workspace_bytes = need - 1
+    rc, err = _call(a1)
     assert rc == M.MVR_E_WORKSPACE and "smaller than" in err
+    prefill16 = M.workspace_size(_args(max_seq_len=1024, max_q_len=256))
+    assert M.workspace_size(_args(max_seq_len=1024, max_q_len=256, page_size=3, max_pages_per_seq=342)) >= \
+        2 * pool + 2 * 64 * 4 + prefill16
     # A page size that does not cover max_seq_len is still the reference's error.
     rc, err = _call(_args(max_seq_len=1024, page_size=3, max_pages_per_seq=300))
     assert rc == M.MVR_E_PAGES_UNCOVERED and "leaving 124 tokens uncovered" in err
@@ -474,13 +480,13 @@ def test_workloads_match_stated_sizes():
 
 
 def test_noalloc_refuses_calls_larger_than_its_scratch():
-    """A page size of 5 repacks the batch's K/V into the scratch: 64 sequences of 8K tokens need ~2 GiB, more
+    """One-token pages repack the batch's K/V into the scratch: 64 sequences of 8K tokens need ~2 GiB, more
     than the static scratch holds, so the call returns MVR_E_WORKSPACE before launching anything (or touching a
     device: the refusal needs none, and the dummy addresses are never read)."""
     lib = M.load_library()
     a = M.PagedAttentionArgs()
     a.dtype, a.num_seqs, a.num_q_heads, a.num_kv_heads, a.head_dim = M.DTYPE_F16, 64, 32, 8, 128
-    a.page_size, a.num_pages, a.max_pages_per_seq, a.max_q_len, a.max_seq_len = 5, 1 << 20, 1640, 1, 8192
+    a.page_size, a.num_pages, a.max_pages_per_seq, a.max_q_len, a.max_seq_len = 1, 1 << 20, 8192, 1, 8192
     fake = 1 << 20
     a.q = a.key_pool = a.value_pool = a.block_tables = a.seq_lens = a.cu_q_lens = a.out = fake
     a.q_stride_head, a.q_stride_token, a.out_stride_head, a.out_stride_token = 64 * 128, 128, 64 * 128, 128

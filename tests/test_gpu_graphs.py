@@ -51,7 +51,9 @@ CASES = {
     "prefill-key-splits-f16": lambda: _ragged("prefill f16", "f16", 32, 8, 128, [4000], [130]),
     "prefill-key-splits-f32": lambda: _ragged("prefill f32", "f32", 32, 8, 128, [4000], [130]),
     "prefill-d64-f16": lambda: _ragged("prefill d64", "f16", 14, 2, 64, [2048, 2048], [256, 200]),
-    "repacked-page-size-5": lambda: _ragged("page size 5", "f16", 32, 8, 128, [700, 97, 1500], [1, 5, 1],
+    "page-size-5-in-place": lambda: _ragged("page size 5", "f16", 32, 8, 128, [700, 97, 1500], [1, 5, 1],
+                                            page_size=5),
+    "repacked-page-size-5": lambda: _ragged("page size 5 prefill", "f16", 32, 8, 128, [700, 300], [1, 100],
                                             page_size=5),
 }
 

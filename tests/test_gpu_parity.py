@@ -462,11 +462,13 @@ def _same_tokens_two_page_sizes(seed, dtype, hq, hkv, d, seq_lens, q_lens, page_
     return q, layouts
 
 
-@pytest.mark.parametrize("page_size", [2, 3, 5, 24, 40])
+@pytest.mark.parametrize("page_size", [1, 2, 3, 5, 8, 24, 40])
 @pytest.mark.parametrize("dtype,hq,hkv,d", [("f16", 32, 8, 128), ("f32", 14, 2, 64)])
 def test_page_sizes_off_16_match_oracle_and_16_token_pages(page_size, dtype, hq, hkv, d):
-    # Decode and verify rows in one ragged batch; page sizes that are not a multiple of 16 are repacked into
-    # 16-token pages in the workspace, so the result equals the same tokens stored in 16-token pages bit for bit.
+    # Decode and verify rows in one ragged batch.  Pages of 2 or more tokens that are not a multiple of 16 are
+    # read in place (each token row from its own page), one-token pages repacked into 16-token pages in the
+    # workspace; either way the call takes the plan of the 16-token layout, so the result equals the same
+    # tokens stored in 16-token pages bit for bit.
     q_lens = [1, 5, 1, 3]
     seq_lens = [37 + page_size, 700, 1 + 2 * page_size, 333]
     q, layouts = _same_tokens_two_page_sizes(900 + page_size, dtype, hq, hkv, d, seq_lens, q_lens, page_size)
@@ -487,6 +489,30 @@ def test_page_sizes_off_16_match_oracle_and_16_token_pages(page_size, dtype, hq,
     diff = int(np.count_nonzero(outs[0].view(view) != outs[1].view(view)))
     say(f"[page size {page_size}] {dtype} D={d}: max-abs vs oracle {err:.3e}; {diff} outputs differ from 16-token pages")
     assert err <= (2e-3 if dtype == "f16" else 1e-5) and diff == 0
+
+
+@pytest.mark.parametrize("page_size", [2, 8, 24])
+@pytest.mark.parametrize("dtype,hq,hkv,d", [("f16", 32, 8, 128), ("f32", 32, 8, 128), ("f16", 14, 2, 64)])
+def test_uniform_batch_in_small_pages_matches_oracle(page_size, dtype, hq, hkv, d):
+    # A uniform decode batch, which 16-token pages run as one block-merge launch: in pages of 2, 8 or 24 tokens
+    # it is read in place by the split-context kernel with its merge pass (another partition order, so compared
+    # with the oracle, not bit for bit), the last page of every sequence partly filled.
+    seq_lens = [1000] * 16
+    q_lens = [1] * 16
+    q, layouts = _same_tokens_two_page_sizes(500 + page_size, dtype, hq, hkv, d, seq_lens, q_lens, page_size)
+    P, kp, vp, bt = layouts[0]
+    out = M.paged_attention(torch.from_numpy(q).cuda(), torch.from_numpy(kp).cuda(), torch.from_numpy(vp).cuda(),
+                            torch.from_numpy(bt).cuda(), torch.tensor(seq_lens, dtype=torch.int32).cuda(),
+                            torch.tensor(np.concatenate([[0], np.cumsum(q_lens)]), dtype=torch.int32).cuda(),
+                            max_q_len=1, max_seq_len=1000, sum_seq_lens=int(sum(seq_lens)))
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    ref = O.paged_attention(q, kp, vp, bt, np.asarray(seq_lens, np.int32),
+                            np.concatenate([[0], np.cumsum(q_lens)]).astype(np.int32), hq, hkv, d, P,
+                            dtype=O.F16 if dtype == "f16" else O.F32, num_threads=16)
+    err = float(np.abs(got.astype(np.float64) - ref).max())
+    say(f"[small pages {page_size}] {dtype} D={d}: max-abs vs oracle {err:.3e}")
+    assert np.isfinite(got).all() and err <= (2e-3 if dtype == "f16" else 1e-5)
 
 
 @pytest.mark.parametrize("page_size", [48, 80, 272])

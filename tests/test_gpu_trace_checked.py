@@ -80,7 +80,8 @@ def _every_entry_point(out_path):
         t = W.device_tensors(w, None, seed=3)
         outs[name] = M.paged_attention(t["q"], t["key_pool"], t["value_pool"], t["block_tables"], t["seq_lens"],
                                        t["cu_q_lens"], max_q_len=w.max_q_len, max_seq_len=w.max_seq_len)
-    # page size 5: repacked into 16-token pages first
+    # page size 5: a decode call reads the pages in place; a prefill-sized call is repacked into 16-token pages
+    # first
     g = torch.Generator(device="cuda").manual_seed(11)
     kp = torch.randn((40, 1, 2, 5, 64), generator=g, device="cuda").half()
     vp = torch.randn((40, 1, 2, 5, 64), generator=g, device="cuda").half()
@@ -88,7 +89,10 @@ def _every_entry_point(out_path):
     bt = torch.arange(40, dtype=torch.int32, device="cuda").flip(0).reshape(2, 20).contiguous()
     sl = torch.tensor([97, 60], dtype=torch.int32, device="cuda")
     cu = torch.tensor([0, 1, 2], dtype=torch.int32, device="cuda")
-    outs["repacked"] = M.paged_attention(q, kp, vp, bt, sl, cu, max_q_len=1, max_seq_len=97)
+    outs["pages5"] = M.paged_attention(q, kp, vp, bt, sl, cu, max_q_len=1, max_seq_len=97)
+    q30 = torch.randn((14, 31, 64), generator=g, device="cuda").half()
+    cu30 = torch.tensor([0, 30, 31], dtype=torch.int32, device="cuda")
+    outs["repacked"] = M.paged_attention(q30, kp, vp, bt, sl, cu30, max_q_len=30, max_seq_len=97)
     # request-level entry
     lay = M.PagedCacheLayout(kp, vp, bt[0, :20].contiguous(), 5, 97)
     outs["request"] = M.forward_paged_attention(q[:, :1].unsqueeze(0).contiguous(), lay, 14, 2, 64, 96, 1)
@@ -213,7 +217,7 @@ def test_roctx_ranges_leave_every_entry_point_bit_identical():
         assert _run_child("entry-points", off, _child_env(MVR_ENABLE_ROCTX="false")).returncode == 0
         assert _run_child("entry-points", on, _child_env(MVR_ENABLE_ROCTX="true")).returncode == 0
         a, b = np.load(off), np.load(on)
-        assert sorted(a.files) == sorted(b.files) and len(a.files) == 9
+        assert sorted(a.files) == sorted(b.files) and len(a.files) == 10
         for k in a.files:
             assert np.array_equal(a[k].view(np.uint8), b[k].view(np.uint8)), k
 

@@ -70,13 +70,15 @@ def _long_prefill(dtype):
     return W.Workload(f"prefill key splits {dtype}", dtype, 32, 8, 128, 16, n + 3, 0.3, lens, qlens, bt, 9)
 
 
-@pytest.mark.parametrize("case", ["repacked-page-size-5", "mixed-with-hints", "block-merge", "prefill", "prefill-f32",
-                                  "prefill-key-splits-f16", "prefill-key-splits-f32"])
+@pytest.mark.parametrize("case", ["page-size-5-in-place", "repacked-page-size-5", "mixed-with-hints", "block-merge",
+                                  "prefill", "prefill-f32", "prefill-key-splits-f16", "prefill-key-splits-f32"])
 def test_noalloc_equals_workspace_call_on_every_plan(case):
-    if case == "repacked-page-size-5":
-        g = torch.Generator(device="cuda").manual_seed(3)
+    if case in ("page-size-5-in-place", "repacked-page-size-5"):
+        # decode and verify rows read 5-token pages in place; with a 100-token chunk the call is prefill-sized
+        # and repacks them into 16-token pages in the scratch first
         hq, hkv, d, P = 32, 8, 128, 5
         lens = np.array([700, 97, 1500], np.int32)
+        qlens = np.array([1, 5, 1] if case == "page-size-5-in-place" else [1, 5, 100], np.int32)
         need = [-(-int(L) // P) for L in lens]
         bt = np.zeros((3, max(need)), np.int32)
         perm = np.random.default_rng(4).permutation(sum(need) + 2).astype(np.int32)
@@ -84,8 +86,7 @@ def test_noalloc_equals_workspace_call_on_every_plan(case):
         for s, n in enumerate(need):
             bt[s, :n] = perm[used:used + n]
             used += n
-        w = W.Workload("page size 5", "f16", hq, hkv, d, P, sum(need) + 2, 0.3, lens, np.array([1, 5, 1], np.int32),
-                       bt, 3)
+        w = W.Workload("page size 5", "f16", hq, hkv, d, P, sum(need) + 2, 0.3, lens, qlens, bt, 3)
         t = W.device_tensors(w, None, seed=3)
     elif case == "mixed-with-hints":
         w = W.llama3_8b_mixed_decode_prefill_f16(num_decode=15, decode_ctx=4096)
