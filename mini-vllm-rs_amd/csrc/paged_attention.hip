@@ -593,6 +593,7 @@ __global__ __launch_bounds__(kWaveSize* WPB, (kernel_min_blocks<Tr, NB, DEPTH, W
       for (int i = 0; i <= Tr::kLoads; i++) pg[i] = 0;
 #pragma unroll
       for (int j = 0; j < kTpWindow; j++) {
+        if (j > 0 && pf + j > pl) break; // the chunk's pages end here (wave-uniform)
         const int page = __builtin_amdgcn_readfirstlane(bt[min(pf + j, pl)]);
 #pragma unroll
         for (int i = 0; i <= Tr::kLoads; i++) {
