@@ -714,8 +714,8 @@ int launch_call(const CallPlan& c, char* ws) {
 }
 
 // Page sizes that are not a multiple of 16 (the reference allows any
-// per_page_token_count; its own tests use 2 and 3): the kernels read whole
-// 16-token chunks of one page, so such a call first repacks every sequence's
+// per_page_token_count; its own tests use 2 and 3) in a call that cannot read
+// them in place (needs_repack): the call first repacks every sequence's
 // tokens into 16-token pages in the workspace (launch_repack_pages: pages16
 // pages per sequence at fixed stride, plus their block table), then runs the
 // plan of that layout.  The attention is the same (only where the keys live
