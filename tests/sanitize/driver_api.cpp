@@ -110,7 +110,7 @@ static void check_scalar_errors() {
 static void check_planning() {
   const int dtypes[] = {MVR_DTYPE_F32, MVR_DTYPE_F16};
   const int dims[] = {64, 128};
-  const int pages[] = {16, 32, 5, 24};
+  const int pages[] = {16, 32, 48, 1, 2, 3, 5, 8, 24};
   struct Shape {
     int num_seqs, hq, hkv, max_q, max_seq;
   } shapes[] = {{1, 14, 2, 1, 512},  {8, 14, 2, 1, 4096},    {64, 32, 8, 1, 8192},
@@ -131,6 +131,8 @@ static void check_planning() {
           int64_t sum = 0;
           for (int v : t.seq_lens) sum += v;
           a.sum_seq_lens = sum;
+          (void)mvr_paged_attention_workspace_size(&a);
+          a.total_q = t.cu.back(); // the plans guessed from the token count (no host tables)
           (void)mvr_paged_attention_workspace_size(&a);
           std::vector<int32_t> sl(t.seq_lens), cu(t.cu); // exact sizes: num_seqs and num_seqs + 1
           a.seq_lens_host = sl.data();
