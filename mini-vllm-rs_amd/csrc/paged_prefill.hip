@@ -70,13 +70,6 @@ struct SeqRows {
   int seq_len, q_start, q_len, key_end; // keys [0, key_end) belong to this call
 };
 
-// Tile barrier: waits until at most kNewer of this wavefront's direct-to-LDS
-// tile loads are in flight and its LDS reads have returned, then meets the
-// other wavefronts.  (__syncthreads() would wait for every load, vmcnt(0),
-// and drain the prefetch.)  The wait is the compiler's own s_waitcnt, so its
-// bookkeeping of the direct-to-LDS loads stays exact; the empty asm
-// statements keep memory accesses from moving across the barrier without
-// any further wait.
 // 16 bytes per lane from one KV page straight into LDS at lds + 16 * lane
 // (buffer_load_dwordx4 ... lds).  The page's base address is wave-uniform
 // (a buffer resource in scalar registers) and each lane adds its byte offset
@@ -95,6 +88,13 @@ __device__ __forceinline__ void load_page_to_lds16(const void* page, uint32_t pa
   __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_void*)lds, 16, byte_offset, 0, 0, 0);
 }
 
+// Tile barrier: waits until at most kNewer of this wavefront's direct-to-LDS
+// tile loads are in flight and its LDS reads have returned, then meets the
+// other wavefronts.  (__syncthreads() would wait for every load, vmcnt(0),
+// and drain the prefetch.)  The wait is the compiler's own s_waitcnt, so its
+// bookkeeping of the direct-to-LDS loads stays exact; the empty asm
+// statements keep memory accesses from moving across the barrier without
+// any further wait.
 template <int kNewer>
 __device__ __forceinline__ void tile_barrier() {
   __builtin_amdgcn_s_waitcnt((kNewer & 0xF) | ((kNewer >> 4) << 14) | (0x7 << 4)); // vmcnt(n) expcnt(7) lgkmcnt(0)
@@ -149,7 +149,7 @@ struct Tile {
   static constexpr int kChunkElems = 16 / (int)sizeof(T);            // elements per 16-byte chunk
   static constexpr int kChunksPerRow = D / kChunkElems;              // 16-byte chunks per token row
   static constexpr int kChunks = kSuperTokens * kChunksPerRow;       // per K (or V) stage
-  static constexpr int kChunksPerThread = kChunks / (kWaves * 64);   // f16: 2 at D=128, 1 at D=64; f32: 4, 2
+  static constexpr int kChunksPerThread = kChunks / (kWaves * 64);   // 4 at D=128, 2 at D=64 (F16 and F32)
   static constexpr int kElems = kSuperTokens * D;
   // V: 32-byte pieces per row, XOR-swizzled with the row.  A transposed read
   // is served per half-wavefront: 4 rows x 2 adjacent pieces, which must land
@@ -701,10 +701,16 @@ __device__ __forceinline__ void prefill_tile_serial(const PrefillParams& p, cons
           *reinterpret_cast<half4*>(slice + row * D + chunk * 8 + 4 * hh) = v4;
         }
       constexpr int kRowsPerRead = 64 / kChunksPerRow;
-      const int cc = l % kChunksPerRow;
+      // The lane index is opaque to the optimiser here, so the read offsets
+      // below are computed where they are used, not hoisted to the kernel's
+      // entry, where (in the catch-up loop) they were spilled to a private
+      // segment.
+      int le = l;
+      asm volatile("" : "+v"(le));
+      const int cc = le % kChunksPerRow;
 #pragma unroll
       for (int k = 0; k < kRowsPerWave / kRowsPerRead; k++) {
-        const int rr = k * kRowsPerRead + l / kChunksPerRow; // row of the wavefront's 32
+        const int rr = k * kRowsPerRead + le / kChunksPerRow; // row of the wavefront's 32
         const half8 v8 = *reinterpret_cast<const half8*>(slice + rr * D + (cc ^ (rr & (kChunksPerRow - 1))) * 8);
         const int rho_w = rt * kBlockRows + rw * kRowsPerWave + rr;
         if (rho_w < rows) {
