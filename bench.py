@@ -356,6 +356,19 @@ def measure_decode_map(W, M, torch, steps, warmup):
     return rows
 
 
+HEAD_DIMS = (32, 64, 96, 128, 160, 192, 224, 256)
+
+
+def measure_head_dims(W, M, torch, steps, warmup):
+    """The headline decode shape (64 x 8192 tokens, 32 Q / 8 KV heads, F16) at every supported head dimension:
+    64 and 128 take the planner's full set of plans, the others the split-context kernel with its merge pass."""
+    res = {}
+    for d in HEAD_DIMS:
+        log(f"[bench] decode at head_dim {d}")
+        res[str(d)] = measure(W, M, torch, lambda: W.decode_b64_8k_head_dim_f16(d), steps, warmup)
+    return res
+
+
 def measure_append(W, M, torch, cfg, steps, warmup):
     w = W.CONFIGS[cfg]()
     t = W.device_tensors(w, None)
@@ -386,6 +399,8 @@ def main():
     ap.add_argument("--decode-map", action="store_true",
                     help="time only ragged against uniform decode batches of about equal bytes (Llama-3-8B, F16)")
     ap.add_argument("--f32", action="store_true", help="with --only-config 4: the same chunked prefill in F32")
+    ap.add_argument("--head-dims", action="store_true",
+                    help="time only the headline decode shape at every supported head dimension")
     a = ap.parse_args()
     if a.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {a.gpus} is not supported: the attention path runs on one "
@@ -410,6 +425,9 @@ def main():
         return
     if a.decode_map:
         print(json.dumps({"decode_map": measure_decode_map(W, M, torch, a.steps, a.warmup)}), flush=True)
+        return
+    if a.head_dims:
+        print(json.dumps({"head_dims": measure_head_dims(W, M, torch, a.steps, a.warmup)}), flush=True)
         return
     if a.f32 and a.only_config != 4:
         print("--f32 goes with --only-config 4", file=sys.stderr)

@@ -85,7 +85,7 @@ hipError_t launch_repack_pages(const void* key_pool, const void* value_pool, con
                                int bt_stride, const int32_t* seq_lens, int single_seq_len, int num_seqs,
                                int num_kv_heads, int page_size, int head_dim, int elem_size, int pages16,
                                void* key16, void* value16, int32_t* bt16, hipStream_t stream) {
-  typedef u32x4 V; // rows of 64 or 128 F16/F32 elements: whole 16-byte vectors, pointers checked 16-byte aligned
+  typedef u32x4 V; // rows of a multiple of 32 F16/F32 elements: whole 16-byte vectors, pointers checked 16-byte aligned
   const int row_vecs = head_dim * elem_size / (int)sizeof(V);
   const int64_t total = (int64_t)num_seqs * num_kv_heads * pages16 * 16 * row_vecs;
   int64_t blocks = (total + 255) / 256;

@@ -127,8 +127,8 @@ int check_scalars(const mvr_paged_attention_args* a) {
   if (a->num_kv_heads < 1 || a->num_q_heads < 1 || a->num_q_heads % a->num_kv_heads != 0)
     return fail(MVR_E_INVALID_ARGUMENT, "num_q_heads %d is not a multiple of num_kv_heads %d", a->num_q_heads,
                 a->num_kv_heads);
-  if (a->head_dim != 64 && a->head_dim != 128)
-    return fail(MVR_E_UNSUPPORTED, "head_dim %d is not supported (64 or 128)", a->head_dim);
+  if (!mvr::head_dim_supported(a->head_dim))
+    return fail(MVR_E_UNSUPPORTED, "head_dim %d is not supported (a multiple of 32 in [32, 256])", a->head_dim);
   if (a->page_size < 1) return fail(MVR_E_INVALID_ARGUMENT, "page_size must be positive");
   if (a->num_pages < 1) return fail(MVR_E_INVALID_ARGUMENT, "num_pages must be positive");
   if (a->max_q_len < 1) return fail(MVR_E_INVALID_ARGUMENT, "each forward input must contain at least one token");
@@ -191,6 +191,9 @@ mvr::PagedAttentionPlan make_plan(const mvr_paged_attention_args* a, bool allow_
   plan.head_dim = a->head_dim;
   const int group = a->num_q_heads / a->num_kv_heads;
   const int64_t rows_max = (int64_t)group * a->max_q_len;
+  // Head dimensions other than 64 and 128: the split-context kernel in its
+  // plain form (16-row tiles, 1-wavefront blocks, the merge pass).
+  const bool all_plans = mvr::head_dim_all_plans(a->head_dim);
   // Many query rows per KV head (chunked prefill): dense contraction, use the
   // LDS-shared 32x32 MFMA kernel (F16 32x32x16, F32 32x32x2).
   // MVR_ATTN_PREFILL_KERNEL=false keeps every call on the split-context kernel.
@@ -201,7 +204,7 @@ mvr::PagedAttentionPlan make_plan(const mvr_paged_attention_args* a, bool allow_
   // Other page sizes reach make_plan only for calls that the split-context
   // kernel serves, which then reads them in place (token pages).
   plan.token_pages = !page_runs;
-  if (allow_prefill && prefill_enabled && (rows_max > 64 || force_prefill) && page_runs) {
+  if (allow_prefill && prefill_enabled && (rows_max > 64 || force_prefill) && page_runs && all_plans) {
     plan.prefill = true;
     plan.row_tiles = (int)((rows_max + mvr::kPrefillBlockRows - 1) / mvr::kPrefillBlockRows);
     const int64_t live_blocks = n_live * a->num_kv_heads * plan.row_tiles;
@@ -224,7 +227,7 @@ mvr::PagedAttentionPlan make_plan(const mvr_paged_attention_args* a, bool allow_
     }
     return plan;
   }
-  plan.row_blocks = rows_max <= 16 ? 1 : 2;
+  plan.row_blocks = rows_max <= 16 || !all_plans ? 1 : 2;
   const int tile_rows = 16 * plan.row_blocks;
   plan.row_tiles = (int)((rows_max + tile_rows - 1) / tile_rows);
   const int max_chunks = (a->max_seq_len + mvr::kChunkTokens - 1) / mvr::kChunkTokens; // the grid covers these
@@ -306,7 +309,7 @@ mvr::PagedAttentionPlan make_plan(const mvr_paged_attention_args* a, bool allow_
   // for head_dim 64 only.  MVR_ATTN_BLOCK_MERGE=false keeps the separate merge.
   static const bool block_merge_enabled = env_bool("MVR_ATTN_BLOCK_MERGE", true);
   plan.block_waves = 0;
-  if (block_merge_enabled && !ragged && plan.row_blocks == 1 && !plan.token_pages) {
+  if (block_merge_enabled && !ragged && plan.row_blocks == 1 && !plan.token_pages && all_plans) {
     const int widest = a->dtype != MVR_DTYPE_F16 ? 4 : a->head_dim == 64 ? 16 : 8;
     for (int w = 4; w <= widest && plan.block_waves == 0; w *= 2)
       if (plan.max_parts <= w && 4 * plan.max_parts >= 3 * w) plan.block_waves = w;
@@ -333,7 +336,7 @@ mvr::PagedAttentionPlan make_plan(const mvr_paged_attention_args* a, bool allow_
   static const bool dense_enabled = env_bool("MVR_ATTN_DENSE_RAGGED", true);
   bool dense = false;
   if (dense_enabled && ragged && plan.row_tiles == 1 && plan.max_parts > 1 && !plan.block_merge && n_live >= 32 &&
-      !plan.token_pages) {
+      !plan.token_pages && all_plans) {
     const int64_t chunk_tokens = (int64_t)mvr::kChunkTokens * plan.chunks_per_part;
     const int64_t est_live = (a->sum_seq_lens + chunk_tokens - 1) / chunk_tokens + n_live / 2;
     dense = est_live * 10 < (int64_t)a->num_seqs * plan.max_parts * 7; // live fraction < 0.7
@@ -381,7 +384,7 @@ mvr::PagedAttentionPlan make_plan(const mvr_paged_attention_args* a, bool allow_
   // MVR_ATTN_DEEP_PIPELINE=false turns it off.
   static const bool deep_enabled = env_bool("MVR_ATTN_DEEP_PIPELINE", true);
   const int elem_bytes = a->dtype == MVR_DTYPE_F16 ? 2 : 4;
-  plan.deep_pipeline = deep_enabled && ragged && !dense && !plan.block_merge && !plan.token_pages &&
+  plan.deep_pipeline = deep_enabled && ragged && !dense && !plan.block_merge && !plan.token_pages && all_plans &&
                        plan.row_blocks == 1 && a->head_dim * elem_bytes <= 256 && plan.chunks_per_part >= 8;
   // No padding of max_parts.  Padding it to a multiple of 32 / gcd(Hkv * row
   // tiles, 32) made partition p of every sequence run on the same XCD (so
@@ -419,7 +422,7 @@ mvr::PagedAttentionPlan make_plan(const mvr_paged_attention_args* a, bool allow_
     static const int unit_waves_override = env_int("MVR_ATTN_UNIT_WAVES", 0);
     if (unit_waves_override == 1 || unit_waves_override == 2 || unit_waves_override == 4)
       plan.unit_waves = unit_waves_override;
-    if (plan.token_pages) plan.unit_waves = 1; // its one instantiation
+    if (plan.token_pages || !all_plans) plan.unit_waves = 1; // their one instantiation
   }
   plan.partial_bytes = 0;
   if (plan.max_parts > 1 && !plan.block_merge) {
@@ -734,7 +737,7 @@ struct RepackPlan {
 // a page) or pages of one token is repacked into 16-token pages first.
 bool needs_repack(const mvr_paged_attention_args* a) {
   if (a->page_size % mvr::kChunkTokens == 0) return false;
-  if (a->page_size < 2) return true;
+  if (a->page_size < 2 || !mvr::head_dim_all_plans(a->head_dim)) return true;
   mvr_paged_attention_args b = *a;
   b.page_size = mvr::kChunkTokens; // the plan the repacked call would take
   const CallPlan c = make_call_plan(&b);

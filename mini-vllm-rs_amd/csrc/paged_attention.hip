@@ -206,12 +206,16 @@ struct F16Traits {
   typedef half8 vreg_t;
   typedef half8 qreg_t;
 
-  // 16-row tiles: 3 wavefronts per SIMD; 32-row tiles: 2.
+  // 16-row tiles: 3 wavefronts per SIMD; 32-row tiles: 2 (wider heads: 2, then 1).
   template <int NB>
-  static constexpr int min_blocks() { return NB == 1 ? 3 : 2; }
+  static constexpr int min_blocks() { return D <= 128 ? (NB == 1 ? 3 : 2) : D <= 192 ? 2 : 1; }
 
-  // 32-byte pieces of an LDS row: D/16; XOR swizzle spreads 16 rows over banks.
-  __device__ static __forceinline__ int swz(int t) { return D == 128 ? (t & 7) : ((t >> 1) & 3); }
+  // 32-byte pieces of an LDS row: D/16; XOR swizzle spreads 16 rows over
+  // banks (within aligned groups of 8 or 4 pieces, so every piece stays in
+  // its row; none where D/16 is not a multiple of 4).
+  __device__ static __forceinline__ int swz(int t) {
+    return D % 128 == 0 ? (t & 7) : D % 64 == 0 ? ((t >> 1) & 3) : 0;
+  }
 
   __device__ static __forceinline__ void load_q(const half_t* row, bool valid, int g, qreg_t (&q)[kQRegs]) {
 #pragma unroll
@@ -301,11 +305,14 @@ struct F32Traits {
   typedef float4v qreg_t;
 
   template <int NB>
-  static constexpr int min_blocks() { return D == 128 ? (NB == 1 ? 2 : 1) : (NB == 1 ? 3 : 2); }
+  static constexpr int min_blocks() {
+    return D == 128 ? (NB == 1 ? 2 : 1) : D <= 64 ? (NB == 1 ? 3 : 2) : D <= 128 ? 2 : 1;
+  }
 
   // 64-byte pieces (16 floats) of an LDS row; rows 4g+j of the four lane
-  // groups land in four different pieces.
-  __device__ static __forceinline__ int swz(int t) { return (t >> 2) & 3; }
+  // groups land in four different pieces (none where D/16 is not a multiple
+  // of 4, so that every piece stays in its row).
+  __device__ static __forceinline__ int swz(int t) { return (D / 16) % 4 == 0 ? ((t >> 2) & 3) : 0; }
 
   __device__ static __forceinline__ void load_q(const float* row, bool valid, int g, qreg_t (&q)[kQRegs]) {
 #pragma unroll
@@ -780,12 +787,18 @@ template <typename T, int D, int NB, bool kWide>
 __global__ __launch_bounds__(256) void merge_partitions_kernel(PagedAttentionParams p) {
   constexpr int kTileRows = 16 * NB;
   constexpr int kBlocksPerTile = kTileRows / kWavesPerBlock;
-  constexpr int kPer = D / kWaveSize; // output elements per lane
+  // Output elements per lane: D/64 over the wavefront, or, where D is not a
+  // multiple of 64, D/32 over lanes 0..31 (the others hold partition weights
+  // only: they re-read lane 31's elements and store nothing).
+  constexpr int kPer = D % kWaveSize == 0 ? D / kWaveSize : D / 32;
+  constexpr int kDimLanes = D / kPer;
   constexpr int kInFlight = 8;
   constexpr int kInFlightWide = kWide ? 32 : kInFlight;
   const int tile = blockIdx.x / kBlocksPerTile;
   const int lr = (blockIdx.x % kBlocksPerTile) * kWavesPerBlock + __builtin_amdgcn_readfirstlane(threadIdx.x / kWaveSize);
   const int l = lane_id();
+  const int ld = kDimLanes == kWaveSize ? l : min(l, kDimLanes - 1); // lane's slice of the row
+  const bool stores = kDimLanes == kWaveSize || l < kDimLanes;
   const int rt = tile % p.row_tiles;
   const int h = (tile / p.row_tiles) % p.num_kv_heads;
   const int b = tile / (p.row_tiles * p.num_kv_heads);
@@ -811,9 +824,10 @@ __global__ __launch_bounds__(256) void merge_partitions_kernel(PagedAttentionPar
   // measured 2% slower on single 32K-token contexts).
   // In groups of 8 rows (one uniform branch per group): a group's rows past
   // the count read the last partial row again (in the tile, an L2 hit) and
-  // are left out of the sum below.
-  constexpr int kFirst = kWide ? 0 : 64 / kPer;
-  const float* const base0 = p.partial_o + prow0 * D + l * kPer;
+  // are left out of the sum below.  (64 / kPer rows, rounded down to whole
+  // groups.)
+  constexpr int kFirst = kWide ? 0 : 64 / kPer / 8 * 8;
+  const float* const base0 = p.partial_o + prow0 * D + ld * kPer;
   float v0[kFirst > 0 ? kFirst : 1][kPer];
 #pragma unroll
   for (int g8 = 0; g8 < kFirst; g8 += 8) {
@@ -847,7 +861,7 @@ __global__ __launch_bounds__(256) void merge_partitions_kernel(PagedAttentionPar
       den += w * ml[1];
     }
     const int cnt = min(kWaveSize, n_parts - j0);
-    const float* base = p.partial_o + (prow0 + (int64_t)j0 * kTileRows) * D + l * kPer;
+    const float* base = p.partial_o + (prow0 + (int64_t)j0 * kTileRows) * D + ld * kPer;
     int jj = 0;
     if (kFirst > 0 && j0 == 0) {
       jj = min(cnt, kFirst);
@@ -903,17 +917,20 @@ __global__ __launch_bounds__(256) void merge_partitions_kernel(PagedAttentionPar
   const float inv = 1.f / den;
   if (p.state_o) {
     const int64_t srow = (int64_t)(h * p.group_size + r) * p.state_tokens + s.q_start + i;
+    if (stores) {
 #pragma unroll
-    for (int e = 0; e < kPer; e++) p.state_o[srow * D + l * kPer + e] = acc[e] * inv;
+      for (int e = 0; e < kPer; e++) p.state_o[srow * D + ld * kPer + e] = acc[e] * inv;
+    }
     if (l == 0) p.state_lse[srow] = m_use + __log2f(den);
     return;
   }
   T* dst = static_cast<T*>(p.out) + (int64_t)(h * p.group_size + r) * p.out_stride_head +
-           (int64_t)(s.q_start + i) * p.out_stride_token + l * kPer;
+           (int64_t)(s.q_start + i) * p.out_stride_token + ld * kPer;
   const int64_t srow = (int64_t)(h * p.group_size + r) * p.state_tokens + s.q_start + i;
   const PrefixWeights pw = prefix_weights(p, b, srow, m_use + __log2f(den));
+  if (!stores) return;
   if (pw.has) {
-    const float* src = p.prefix_o + srow * D + l * kPer;
+    const float* src = p.prefix_o + srow * D + ld * kPer;
 #pragma unroll
     for (int e = 0; e < kPer; e++) dst[e] = (T)((pw.wa * src[e] + pw.wb * (acc[e] * inv)) * pw.inv);
     return;
@@ -927,7 +944,13 @@ __global__ __launch_bounds__(256) void merge_partitions_kernel(PagedAttentionPar
 template <typename Tr, int D, int NB, int WPB>
 hipError_t launch_units(const PagedAttentionPlan& plan, const PagedAttentionParams& params, hipStream_t stream) {
   const int64_t blocks = (plan.num_units + WPB - 1) / WPB;
-  if (plan.token_pages) {
+  if constexpr (!head_dim_all_plans(D)) {
+    // The other head dimensions: the plain variant only.
+    if (plan.token_pages || plan.dense_parts || plan.deep_pipeline) return hipErrorInvalidValue;
+    hipLaunchKernelGGL((paged_attention_kernel<Tr, D, NB, false, false, 2, WPB>), dim3((unsigned)blocks),
+                       dim3(kWaveSize * WPB), 0, stream, params);
+    return hipGetLastError();
+  } else if (plan.token_pages) {
     // planned with one wavefront per block, two chunks in flight, slot == partition
     if (WPB != 1 || plan.dense_parts || plan.deep_pipeline) return hipErrorInvalidValue;
     hipLaunchKernelGGL((paged_attention_kernel<Tr, D, NB, false, false, 2, 1, true>), dim3((unsigned)blocks),
@@ -952,7 +975,7 @@ hipError_t launch_units(const PagedAttentionPlan& plan, const PagedAttentionPara
 
 template <typename Tr, int D, int NB>
 hipError_t launch_typed(const PagedAttentionPlan& plan, const PagedAttentionParams& params, hipStream_t stream) {
-  if constexpr (NB == 1) {
+  if constexpr (NB == 1 && head_dim_all_plans(D)) {
     if (plan.block_merge) {
       // One block of block_waves wavefronts per (sequence, KV head, row tile).
       const int64_t tiles = (int64_t)params.num_seqs * params.num_kv_heads * params.row_tiles;
@@ -982,6 +1005,8 @@ hipError_t launch_typed(const PagedAttentionPlan& plan, const PagedAttentionPara
   hipError_t err;
   if (uw == 1) {
     err = launch_units<Tr, D, NB, 1>(plan, params, stream);
+  } else if constexpr (!head_dim_all_plans(D)) {
+    return hipErrorInvalidValue; // 1-wavefront blocks only
   } else if (uw == 2) {
     err = launch_units<Tr, D, NB, 2>(plan, params, stream);
   } else if (uw == 4) {
@@ -1015,11 +1040,23 @@ hipError_t launch_paged_attention(const PagedAttentionPlan& plan, PagedAttention
     MVR_DISPATCH(F16Traits, 64, 2)
     MVR_DISPATCH(F16Traits, 128, 1)
     MVR_DISPATCH(F16Traits, 128, 2)
+    MVR_DISPATCH(F16Traits, 32, 1)
+    MVR_DISPATCH(F16Traits, 96, 1)
+    MVR_DISPATCH(F16Traits, 160, 1)
+    MVR_DISPATCH(F16Traits, 192, 1)
+    MVR_DISPATCH(F16Traits, 224, 1)
+    MVR_DISPATCH(F16Traits, 256, 1)
   } else {
     MVR_DISPATCH(F32Traits, 64, 1)
     MVR_DISPATCH(F32Traits, 64, 2)
     MVR_DISPATCH(F32Traits, 128, 1)
     MVR_DISPATCH(F32Traits, 128, 2)
+    MVR_DISPATCH(F32Traits, 32, 1)
+    MVR_DISPATCH(F32Traits, 96, 1)
+    MVR_DISPATCH(F32Traits, 160, 1)
+    MVR_DISPATCH(F32Traits, 192, 1)
+    MVR_DISPATCH(F32Traits, 224, 1)
+    MVR_DISPATCH(F32Traits, 256, 1)
   }
 #undef MVR_DISPATCH
   return hipErrorInvalidValue;
@@ -1042,9 +1079,20 @@ int64_t resident_waves_typed() {
     if (known > 0) return known;
   }
   int cus = 0, blocks = 0;
-  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-      hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, paged_attention_kernel<Tr, D, NB>,
-                                                   kWaveSize * kWavesPerBlock, 0) != hipSuccess) {
+  hipError_t err = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+  if (err == hipSuccess) {
+    if constexpr (head_dim_all_plans(D)) {
+      err = hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, paged_attention_kernel<Tr, D, NB>,
+                                                         kWaveSize * kWavesPerBlock, 0);
+    } else {
+      // The variant these head dimensions launch (1-wavefront blocks), in
+      // blocks of kWavesPerBlock wavefronts per CU.
+      err = hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, paged_attention_kernel<Tr, D, NB, false, false, 2, 1>,
+                                                         kWaveSize, 0);
+      blocks /= kWavesPerBlock;
+    }
+  }
+  if (err != hipSuccess) {
     (void)hipGetLastError();
     return 0;
   }
@@ -1067,11 +1115,23 @@ int64_t paged_attention_resident_waves(int dtype, int head_dim, int row_blocks) 
     MVR_OCC(F16Traits, 64, 2)
     MVR_OCC(F16Traits, 128, 1)
     MVR_OCC(F16Traits, 128, 2)
+    MVR_OCC(F16Traits, 32, 1)
+    MVR_OCC(F16Traits, 96, 1)
+    MVR_OCC(F16Traits, 160, 1)
+    MVR_OCC(F16Traits, 192, 1)
+    MVR_OCC(F16Traits, 224, 1)
+    MVR_OCC(F16Traits, 256, 1)
   } else {
     MVR_OCC(F32Traits, 64, 1)
     MVR_OCC(F32Traits, 64, 2)
     MVR_OCC(F32Traits, 128, 1)
     MVR_OCC(F32Traits, 128, 2)
+    MVR_OCC(F32Traits, 32, 1)
+    MVR_OCC(F32Traits, 96, 1)
+    MVR_OCC(F32Traits, 160, 1)
+    MVR_OCC(F32Traits, 192, 1)
+    MVR_OCC(F32Traits, 224, 1)
+    MVR_OCC(F32Traits, 256, 1)
   }
 #undef MVR_OCC
   return 0;

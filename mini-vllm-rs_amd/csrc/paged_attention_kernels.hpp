@@ -12,6 +12,15 @@ constexpr int kChunkTokens = 16;
 constexpr int kWaveSize = 64;
 constexpr int kWavesPerBlock = 4;
 
+// Head dimensions.  64 and 128 (every model shape the reference runs) take
+// every plan: block merge, dense, deep pipeline, token pages and the
+// chunked-prefill kernel.  The other multiples of 32 up to 256 take the
+// split-context kernel with 16-row tiles in 1-wavefront blocks and the merge
+// pass, for every call shape (page sizes that are not a multiple of 16 are
+// repacked first).
+constexpr bool head_dim_supported(int d) { return d >= 32 && d <= 256 && d % 32 == 0; }
+constexpr bool head_dim_all_plans(int d) { return d == 64 || d == 128; }
+
 // One launch of the split-context kernel.  A "unit" is the work of one
 // wavefront: (sequence b, kv head h, row tile rt, context partition part).
 // Rows of a kv head are the grouped query rows rho = r*q_len + i (r = query
@@ -63,7 +72,7 @@ struct PagedAttentionParams {
 // Grid shape chosen by the host.
 struct PagedAttentionPlan {
   int dtype;      // 0 f32, 1 f16
-  int head_dim;   // 64 or 128
+  int head_dim;   // head_dim_supported()
   int row_blocks; // 16-row MFMA blocks per wavefront (1 or 2)
   int row_tiles;
   int chunks_per_part;

@@ -43,7 +43,7 @@ pub struct MvrPagedAttentionArgs {
     pub num_seqs: i32,          // requests packed in the call
     pub num_q_heads: i32,
     pub num_kv_heads: i32,
-    pub head_dim: i32,          // 64 or 128
+    pub head_dim: i32,          // a multiple of 32 in [32, 256]
     pub page_size: i32,         // per_page_token_count
     pub num_pages: i64,         // page_count of each pool
     pub max_pages_per_seq: i32, // row stride of block_tables

@@ -147,6 +147,18 @@ def llama3_8b_decode_b64_8k_f16(batch: int = 64, dtype: str = "f16") -> Workload
                     np.ones(batch, np.int32), bt, seed)
 
 
+def decode_b64_8k_head_dim_f16(head_dim: int, batch: int = 64) -> Workload:
+    """The headline decode shape (batch x 8192 tokens, 32 Q / 8 KV heads, F16, 16-token pages in random order, pool
+    = exact fit) at another head dimension, for timing the head dimensions besides 64 and 128."""
+    seed = SEED_BASE + 17 + head_dim
+    rng = np.random.default_rng(seed)
+    seq_lens = np.full(batch, 8192, np.int32)
+    num_pages = batch * 512
+    bt = _assign_pages(rng, seq_lens, 16, num_pages)
+    return Workload(f"decode f16 b{batch} ctx8192 32/8 heads D{head_dim}", "f16", 32, 8, head_dim, 16, num_pages, 0.3,
+                    seq_lens, np.ones(batch, np.int32), bt, seed)
+
+
 def qwen2_7b_chunked_prefill_f16(dtype: str = "f16") -> Workload:
     """4 sequences, 2048 cached + 256 new tokens, 28 Q / 4 KV, D 128, pages in random order (dtype "f32": the same
     shape in F32)."""

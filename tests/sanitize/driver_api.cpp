@@ -85,7 +85,7 @@ static void check_scalar_errors() {
     void (*edit)(mvr_paged_attention_args&);
   } bad[] = {
       {"dtype", [](mvr_paged_attention_args& a) { a.dtype = 7; }},
-      {"head_dim", [](mvr_paged_attention_args& a) { a.head_dim = 96; }},
+      {"head_dim", [](mvr_paged_attention_args& a) { a.head_dim = 80; }},
       {"heads", [](mvr_paged_attention_args& a) { a.num_q_heads = 30; }},
       {"page_size", [](mvr_paged_attention_args& a) { a.page_size = 0; }},
       {"num_seqs", [](mvr_paged_attention_args& a) { a.num_seqs = 0; }},
@@ -109,7 +109,7 @@ static void check_scalar_errors() {
 // host hints are exact-size heap arrays read by the planner.
 static void check_planning() {
   const int dtypes[] = {MVR_DTYPE_F32, MVR_DTYPE_F16};
-  const int dims[] = {64, 128};
+  const int dims[] = {32, 64, 96, 128, 160, 256};
   const int pages[] = {16, 32, 48, 1, 2, 3, 5, 8, 24};
   struct Shape {
     int num_seqs, hq, hkv, max_q, max_seq;

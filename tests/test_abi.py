@@ -73,7 +73,7 @@ def _call(a):
     ("dtype", 7, M.MVR_E_UNSUPPORTED, "dtype"),
     ("num_seqs", 0, M.MVR_E_INVALID_ARGUMENT, "forward requires at least one request"),
     ("num_kv_heads", 5, M.MVR_E_INVALID_ARGUMENT, "not a multiple"),
-    ("head_dim", 96, M.MVR_E_UNSUPPORTED, "head_dim"),
+    ("head_dim", 80, M.MVR_E_UNSUPPORTED, "head_dim"),
     ("page_size", 0, M.MVR_E_INVALID_ARGUMENT, "page_size must be positive"),
     ("max_q_len", 0, M.MVR_E_INVALID_ARGUMENT, "at least one token"),
     ("max_pages_per_seq", 60, M.MVR_E_PAGES_UNCOVERED, "leaving 64 tokens uncovered"),
@@ -90,6 +90,30 @@ def test_scalar_checks_reject_before_launch(field, value, code, msg):
     assert msg in err
 
 
+@pytest.mark.parametrize("head_dim", [16, 48, 80, 112, 288, 512])
+def test_head_dims_off_the_multiples_of_32_up_to_256_are_refused(head_dim):
+    rc, err = _call(_args(head_dim=head_dim, q_stride_head=64 * head_dim, q_stride_token=head_dim,
+                          out_stride_head=64 * head_dim, out_stride_token=head_dim))
+    assert rc == M.MVR_E_UNSUPPORTED
+    assert f"head_dim {head_dim} is not supported" in err
+
+
+@pytest.mark.parametrize("dtype", [M.DTYPE_F16, M.DTYPE_F32])
+@pytest.mark.parametrize("head_dim", [32, 96, 160, 192, 224, 256])
+@pytest.mark.parametrize("page_size", [16, 5])
+def test_other_head_dims_plan_the_split_kernel_with_its_merge(dtype, head_dim, page_size):
+    # Decode, verification and prefill-sized calls of the head dimensions besides 64 and 128 plan on the host
+    # (no device: the sizing path) as split contexts merged from partials in the workspace, so it is never
+    # empty; page size 5 adds the repack into 16-token pages.
+    lib = M.load_library()
+    for q_len in (1, 5, 100):
+        a = _args(dtype=dtype, head_dim=head_dim, page_size=page_size, max_q_len=q_len, max_seq_len=1024 + q_len,
+                  max_pages_per_seq=(1024 + q_len + page_size - 1) // page_size, q_stride_head=64 * q_len * head_dim,
+                  q_stride_token=head_dim, out_stride_head=64 * q_len * head_dim, out_stride_token=head_dim)
+        size = lib.mvr_paged_attention_workspace_size(ctypes.byref(a))
+        assert size > 0, (head_dim, page_size, q_len, lib.mvr_last_error().decode())
+
+
 def test_errors_are_per_thread_under_concurrent_calls():
     # Several backends (one OS thread each, server/mod.rs:380-391) may call the library at once; each
     # thread must read back its own error.  ctypes drops the GIL around foreign calls, so the
@@ -97,7 +121,7 @@ def test_errors_are_per_thread_under_concurrent_calls():
     import threading
     cases = [("dtype", 7, M.MVR_E_UNSUPPORTED, "dtype"),
              ("num_kv_heads", 5, M.MVR_E_INVALID_ARGUMENT, "not a multiple"),
-             ("head_dim", 96, M.MVR_E_UNSUPPORTED, "head_dim"),
+             ("head_dim", 80, M.MVR_E_UNSUPPORTED, "head_dim"),
              ("max_pages_per_seq", 60, M.MVR_E_PAGES_UNCOVERED, "leaving 64 tokens uncovered"),
              ("q_stride_token", 100, M.MVR_E_INVALID_ARGUMENT, "aligned"),
              ("seq_lens", None, M.MVR_E_INVALID_ARGUMENT, "required"),

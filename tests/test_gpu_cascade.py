@@ -1,16 +1,14 @@
 """GPU parity of cascade (prefix-sharing) attention, mvr_paged_attention_cascade.
 
-Groups of consecutive sequences share their first pages; the prefix is
-attended once per group and merged with each member's suffix.  The result is
-the same attention (an exact split of the softmax sum), so the bar is the
-plain call's: 2e-3 (F16) / 1e-5 (F32) against the oracle, which knows nothing
-of the groups.  Covers the speculative-verification workload's own groups (4 x
-4 sequences sharing 1024 tokens), ragged groups with a lone sequence and a
-group of one, a prefix pass that takes the chunked-prefill kernel (many rows
-per group), F32 and head_dim 64, a call with no group at all, and a decode
-batch of 64 sequences sharing one 8192-token prompt (plain call checked too).  With the sum_prefix_lens
-hint, the verification workload (shared reads 9% of the key reads) runs as the plain call, bit for bit, and
-the shared prompt (86%) still cascades.
+Groups of consecutive sequences share their first pages; the prefix is attended once per group and merged with
+each member's suffix.  The result is the same attention (an exact split of the softmax sum), so the bar is the
+plain call's: 2e-3 (F16) / 1e-5 (F32) against the oracle, which knows nothing of the groups.  Covers the
+speculative-verification workload's own groups (4 x 4 sequences sharing 1024 tokens), ragged groups with a lone
+sequence and a group of one, a prefix pass that takes the chunked-prefill kernel (many rows per group), F32 and
+head dimensions 64, 96, 160 and 256 (the last three with both passes on the split-context kernel), a call with no
+group at all, and a decode batch of 64 sequences sharing one 8192-token prompt (plain call checked too).  With
+the sum_prefix_lens hint, the verification workload (shared reads 9% of the key reads) runs as the plain call,
+bit for bit, and the shared prompt (86%) still cascades.
 """
 import math
 import sys
@@ -130,7 +128,8 @@ def shared_prefix_workload(dtype, d, page_size, q_lens, cached, groups, hq=8, hk
     return wk
 
 
-@pytest.mark.parametrize("dtype,d", [("f16", 128), ("f16", 64), ("f32", 64), ("f32", 128)])
+@pytest.mark.parametrize("dtype,d", [("f16", 128), ("f16", 64), ("f32", 64), ("f32", 128), ("f16", 96), ("f32", 160),
+                                     ("f16", 256)])
 def test_ragged_groups_match_oracle(dtype, d):
     # groups: seqs 0-2 share 48 tokens, seq 3 shares nothing (prefix-0 group), seqs 4-5 share 32, seq 6 is a group
     # of one (prefix 64), seq 7 follows the last group
