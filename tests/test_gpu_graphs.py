@@ -55,6 +55,7 @@ CASES = {
                                             page_size=5),
     "repacked-page-size-5": lambda: _ragged("page size 5 prefill", "f16", 32, 8, 128, [700, 300], [1, 100],
                                             page_size=5),
+    "head-dim-96-f32": lambda: _ragged("head_dim 96", "f32", 32, 8, 96, [700, 97, 1500], [1, 5, 40]),
 }
 
 

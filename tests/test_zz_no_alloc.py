@@ -70,13 +70,15 @@ def _long_prefill(dtype):
     return W.Workload(f"prefill key splits {dtype}", dtype, 32, 8, 128, 16, n + 3, 0.3, lens, qlens, bt, 9)
 
 
-@pytest.mark.parametrize("case", ["page-size-5-in-place", "repacked-page-size-5", "mixed-with-hints", "block-merge",
-                                  "prefill", "prefill-f32", "prefill-key-splits-f16", "prefill-key-splits-f32"])
+@pytest.mark.parametrize("case", ["page-size-5-in-place", "repacked-page-size-5", "head-dim-96-repacked",
+                                  "mixed-with-hints", "block-merge", "prefill", "prefill-f32", "prefill-key-splits-f16",
+                                  "prefill-key-splits-f32"])
 def test_noalloc_equals_workspace_call_on_every_plan(case):
-    if case in ("page-size-5-in-place", "repacked-page-size-5"):
+    if case in ("page-size-5-in-place", "repacked-page-size-5", "head-dim-96-repacked"):
         # decode and verify rows read 5-token pages in place; with a 100-token chunk the call is prefill-sized
-        # and repacks them into 16-token pages in the scratch first
-        hq, hkv, d, P = 32, 8, 128, 5
+        # and repacks them into 16-token pages in the scratch first (head_dim 96: always repacked, then the
+        # split-context kernel's partials in the scratch too)
+        hq, hkv, d, P = 32, 8, 96 if case == "head-dim-96-repacked" else 128, 5
         lens = np.array([700, 97, 1500], np.int32)
         qlens = np.array([1, 5, 1] if case == "page-size-5-in-place" else [1, 5, 100], np.int32)
         need = [-(-int(L) // P) for L in lens]
