@@ -360,12 +360,14 @@ HEAD_DIMS = (32, 64, 96, 128, 160, 192, 224, 256)
 
 
 def measure_head_dims(W, M, torch, steps, warmup):
-    """The headline decode shape (64 x 8192 tokens, 32 Q / 8 KV heads, F16) at every supported head dimension:
-    64 and 128 take the planner's full set of plans, the others the split-context kernel with its merge pass."""
+    """The headline decode shape (64 x 8192 tokens, 32 Q / 8 KV heads, F16) and the Qwen2-7B chunked-prefill shape
+    at every supported head dimension: 64 and 128 take the planner's full set of plans (the prefill kernel for the
+    chunk), the others the split-context kernel with its merge pass."""
     res = {}
     for d in HEAD_DIMS:
-        log(f"[bench] decode at head_dim {d}")
-        res[str(d)] = measure(W, M, torch, lambda: W.decode_b64_8k_head_dim_f16(d), steps, warmup)
+        log(f"[bench] decode and prefill chunk at head_dim {d}")
+        res[str(d)] = dict(decode=measure(W, M, torch, lambda: W.decode_b64_8k_head_dim_f16(d), steps, warmup),
+                           prefill=measure(W, M, torch, lambda: W.chunked_prefill_head_dim_f16(d), steps, warmup))
     return res
 
 

@@ -159,6 +159,14 @@ def decode_b64_8k_head_dim_f16(head_dim: int, batch: int = 64) -> Workload:
                     seq_lens, np.ones(batch, np.int32), bt, seed)
 
 
+def chunked_prefill_head_dim_f16(head_dim: int) -> Workload:
+    """The Qwen2-7B chunked-prefill shape (4 x 256 new tokens on 2048 cached, 28 Q / 4 KV heads, F16) at another
+    head dimension."""
+    w = qwen2_7b_chunked_prefill_f16()
+    return Workload(f"qwen2-7b-shaped chunked prefill f16 D{head_dim}", "f16", w.num_q_heads, w.num_kv_heads, head_dim,
+                    w.page_size, w.num_pages, w.value_scale, w.seq_lens, w.q_lens, w.block_tables, w.seed + head_dim)
+
+
 def qwen2_7b_chunked_prefill_f16(dtype: str = "f16") -> Workload:
     """4 sequences, 2048 cached + 256 new tokens, 28 Q / 4 KV, D 128, pages in random order (dtype "f32": the same
     shape in F32)."""
