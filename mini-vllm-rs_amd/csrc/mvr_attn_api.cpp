@@ -192,7 +192,8 @@ mvr::PagedAttentionPlan make_plan(const mvr_paged_attention_args* a, bool allow_
   const int group = a->num_q_heads / a->num_kv_heads;
   const int64_t rows_max = (int64_t)group * a->max_q_len;
   // Head dimensions other than 64 and 128: the split-context kernel in its
-  // plain form (16-row tiles, 1-wavefront blocks, the merge pass).
+  // plain form (16-row tiles, 1-wavefront blocks, the merge pass), and the
+  // prefill kernel where it takes them.
   const bool all_plans = mvr::head_dim_all_plans(a->head_dim);
   // Many query rows per KV head (chunked prefill): dense contraction, use the
   // LDS-shared 32x32 MFMA kernel (F16 32x32x16, F32 32x32x2).
@@ -204,7 +205,8 @@ mvr::PagedAttentionPlan make_plan(const mvr_paged_attention_args* a, bool allow_
   // Other page sizes reach make_plan only for calls that the split-context
   // kernel serves, which then reads them in place (token pages).
   plan.token_pages = !page_runs;
-  if (allow_prefill && prefill_enabled && (rows_max > 64 || force_prefill) && page_runs && all_plans) {
+  if (allow_prefill && prefill_enabled && (rows_max > 64 || force_prefill) && page_runs &&
+      mvr::prefill_head_dim_supported(a->head_dim, a->dtype == MVR_DTYPE_F32)) {
     plan.prefill = true;
     plan.row_tiles = (int)((rows_max + mvr::kPrefillBlockRows - 1) / mvr::kPrefillBlockRows);
     const int64_t live_blocks = n_live * a->num_kv_heads * plan.row_tiles;

@@ -158,12 +158,19 @@ struct Tile {
   // cycles per read).  At D=64 two rows share a 256-byte bank line and
   // row&3 is already conflict-free.
   // F32 V rows are not swizzled: each half-wavefront reads one whole token row.
-  __device__ static __forceinline__ int vswz(int t) { return kF32 ? 0 : D == 128 ? 2 * (t & 3) : (t & 3); }
+  // Other head dimensions keep the XOR inside an aligned group of 4 (D a
+  // multiple of 64) or 2 pieces, so that every piece stays in its row.
+  __device__ static __forceinline__ int vswz(int t) {
+    return kF32 ? 0 : D % 128 == 0 ? 2 * (t & 3) : D % 64 == 0 ? (t & 3) : (t & 1);
+  }
   // K: the 16 lanes of a ds_read_b128 pass read one chunk of 16 different
   // rows; XOR with row%16 spreads them over all banks.  Only the low four
-  // chunk bits are swizzled, so at F32 D=128 the upper 16 chunks of a row are
-  // an immediate offset from the lower ones.
-  __device__ static __forceinline__ int kswz(int t) { return t & (kChunksPerRow < 16 ? kChunksPerRow - 1 : 15); }
+  // chunk bits are swizzled, so at F32 D=128 the upper 16 chunks of a row
+  // are an immediate offset from the lower ones.  Rows whose
+  // chunk count is not a power of two swizzle inside aligned groups of its
+  // largest power-of-two factor, so that every chunk stays in its row.
+  static constexpr int kSwzGroup = (kChunksPerRow & -kChunksPerRow) < 16 ? (kChunksPerRow & -kChunksPerRow) : 16;
+  __device__ static __forceinline__ int kswz(int t) { return t & (kSwzGroup - 1); }
 };
 
 // One (sequence, kv head, 128-row tile, key split): each step stages one
@@ -685,38 +692,58 @@ __device__ __forceinline__ void prefill_tile_serial(const PrefillParams& p, cons
       // chunk.  The slice swizzles 16-byte chunks with the row (chunk ^ row %
       // chunks), so neither the 8-byte writes nor the 16-byte reads collide
       // in LDS banks.  A wavefront's LDS accesses complete in order, so its
-      // reads see its writes.
+      // reads see its writes.  (Head dimensions whose rows do not tile a
+      // wavefront's 64 lanes in whole 16-byte chunks, or whose V stage is
+      // too small or carries part of the hand-off, store straight from the
+      // MFMA layout.)
       constexpr int kChunksPerRow = D / 8;
-      static_assert(kF32 || kRowWaves * kRowsPerWave * D <= TL::kElems, "output staging exceeds the V stage");
-      half_t* slice = reinterpret_cast<half_t*>(v_lds0) + rw * kRowsPerWave * D;
-      const float inv = valid ? 1.f / ltot : 0.f;
-      const int row = l & 31;
+      constexpr bool kStaged = 64 % kChunksPerRow == 0 && kRowWaves * kRowsPerWave * D <= TL::kElems &&
+                               (D / 32) * kRowWaves * 1024 <= 2 * kStageFloats;
+      if constexpr (!kStaged) {
+        if (valid) {
+          const float inv = 1.f / ltot;
+          half_t* dst = static_cast<half_t*>(p.out) + (int64_t)(h * p.group_size + r) * p.out_stride_head +
+                        (int64_t)(s.q_start + i) * p.out_stride_token;
 #pragma unroll
-      for (int n = 0; n < D / 32; n++)
+          for (int n = 0; n < D / 32; n++)
 #pragma unroll
-        for (int a = 0; a < 4; a++) {
-          const half4 v4 = {(half_t)(o[n][4 * a] * inv), (half_t)(o[n][4 * a + 1] * inv),
-                            (half_t)(o[n][4 * a + 2] * inv), (half_t)(o[n][4 * a + 3] * inv)};
-          const int chunk = (4 * n + a) ^ (row & (kChunksPerRow - 1));
-          *reinterpret_cast<half4*>(slice + row * D + chunk * 8 + 4 * hh) = v4;
+            for (int a = 0; a < 4; a++)
+              *reinterpret_cast<half4*>(dst + 32 * n + 8 * a + 4 * hh) =
+                  half4{(half_t)(o[n][4 * a] * inv), (half_t)(o[n][4 * a + 1] * inv), (half_t)(o[n][4 * a + 2] * inv),
+                        (half_t)(o[n][4 * a + 3] * inv)};
         }
-      constexpr int kRowsPerRead = 64 / kChunksPerRow;
-      // The lane index is opaque to the optimiser here, so the read offsets
-      // below are computed where they are used, not hoisted to the kernel's
-      // entry, where (in the catch-up loop) they were spilled to a private
-      // segment.
-      int le = l;
-      asm volatile("" : "+v"(le));
-      const int cc = le % kChunksPerRow;
+      } else {
+        half_t* slice = reinterpret_cast<half_t*>(v_lds0) + rw * kRowsPerWave * D;
+        const float inv = valid ? 1.f / ltot : 0.f;
+        const int row = l & 31;
 #pragma unroll
-      for (int k = 0; k < kRowsPerWave / kRowsPerRead; k++) {
-        const int rr = k * kRowsPerRead + le / kChunksPerRow; // row of the wavefront's 32
-        const half8 v8 = *reinterpret_cast<const half8*>(slice + rr * D + (cc ^ (rr & (kChunksPerRow - 1))) * 8);
-        const int rho_w = rt * kBlockRows + rw * kRowsPerWave + rr;
-        if (rho_w < rows) {
-          const int rr_r = rho_w / s.q_len, rr_i = rho_w % s.q_len;
-          *reinterpret_cast<half8*>(static_cast<half_t*>(p.out) + (int64_t)(h * p.group_size + rr_r) * p.out_stride_head +
-                                    (int64_t)(s.q_start + rr_i) * p.out_stride_token + cc * 8) = v8;
+        for (int n = 0; n < D / 32; n++)
+#pragma unroll
+          for (int a = 0; a < 4; a++) {
+            const half4 v4 = {(half_t)(o[n][4 * a] * inv), (half_t)(o[n][4 * a + 1] * inv),
+                              (half_t)(o[n][4 * a + 2] * inv), (half_t)(o[n][4 * a + 3] * inv)};
+            const int chunk = (4 * n + a) ^ (row & (kChunksPerRow - 1));
+            *reinterpret_cast<half4*>(slice + row * D + chunk * 8 + 4 * hh) = v4;
+          }
+        constexpr int kRowsPerRead = 64 / kChunksPerRow;
+        // The lane index is opaque to the optimiser here, so the read offsets
+        // below are computed where they are used, not hoisted to the kernel's
+        // entry, where (in the catch-up loop) they were spilled to a private
+        // segment.
+        int le = l;
+        asm volatile("" : "+v"(le));
+        const int cc = le % kChunksPerRow;
+#pragma unroll
+        for (int k = 0; k < kRowsPerWave / kRowsPerRead; k++) {
+          const int rr = k * kRowsPerRead + le / kChunksPerRow; // row of the wavefront's 32
+          const half8 v8 = *reinterpret_cast<const half8*>(slice + rr * D + (cc ^ (rr & (kChunksPerRow - 1))) * 8);
+          const int rho_w = rt * kBlockRows + rw * kRowsPerWave + rr;
+          if (rho_w < rows) {
+            const int rr_r = rho_w / s.q_len, rr_i = rho_w % s.q_len;
+            half_t* dst = static_cast<half_t*>(p.out) + (int64_t)(h * p.group_size + rr_r) * p.out_stride_head +
+                          (int64_t)(s.q_start + rr_i) * p.out_stride_token;
+            *reinterpret_cast<half8*>(dst + cc * 8) = v8;
+          }
         }
       }
     }
@@ -737,6 +764,15 @@ __device__ __forceinline__ void prefill_tile_serial(const PrefillParams& p, cons
   }
 }
 
+// Key tile per group and step: 64 tokens for F16 (the per-tile row max,
+// rescale test, barrier and block-table work spread over twice the keys:
+// 48.8 -> 47.0 us on the Qwen2-7B chunk, 32.3 -> 31.5 us on a Qwen2-0.5B-shape
+// chunk), 32 for F32, whose 64-token stages would not fit in LDS.
+template <int D, typename T>
+constexpr int prefill_tile_tokens() {
+  return sizeof(T) == 4 ? 32 : 64;
+}
+
 // Main grid: block x covers (sequence, kv head, row tile, key split) of the
 // main range.  XCD-aware decode: block x runs on XCD x % 8 and all blocks of
 // one (sequence, kv head) pair sit on the same XCD, so their shared K/V stays
@@ -745,7 +781,7 @@ __device__ __forceinline__ void prefill_tile_serial(const PrefillParams& p, cons
 template <int D, typename T>
 __device__ __forceinline__ void prefill_tile(const PrefillParams& p, const SeqRows& s, int b, int h, int rt, int split,
                                              int kv_splits) {
-  prefill_tile_serial<D, T, sizeof(T) == 4 ? 32 : 64>(p, s, b, h, rt, split, kv_splits);
+  prefill_tile_serial<D, T, prefill_tile_tokens<D, T>()>(p, s, b, h, rt, split, kv_splits);
 }
 
 __host__ __device__ __forceinline__ int64_t prefill_main_blocks(const PrefillParams& p) {
@@ -832,13 +868,18 @@ constexpr int merge_rows() {
 }
 template <int D, typename T, int TT>
 __global__ __launch_bounds__(256) void prefill_merge_kernel(PrefillParams p) {
-  constexpr int kPer = D / 64;
+  // Output elements per lane: D/64 over the wavefront, or, where D is not a
+  // multiple of 64, D/32 over lanes 0..31 (the others hold split weights
+  // only: they re-read lane 31's elements and store nothing).
+  constexpr int kPer = D % 64 == 0 ? D / 64 : D / 32;
+  constexpr int kDimLanes = D / kPer;
   constexpr int kMergeRows = merge_rows<D>();
   constexpr int kBlocksPerTile = kBlockRows / (kMergeWaves * kMergeRows);
   const int tile = blockIdx.x / kBlocksPerTile; // (b - seq_lo, h, rt)
   const int lr0 = ((blockIdx.x % kBlocksPerTile) * kMergeWaves + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6)) *
                   kMergeRows;
   const int l = threadIdx.x & 63;
+  const int ld = kDimLanes == 64 ? l : min(l, kDimLanes - 1); // lane's slice of the row
   const int rt = tile % p.row_tiles;
   const int h = (tile / p.row_tiles) % p.num_kv_heads;
   const int b = p.seq_lo + tile / (p.row_tiles * p.num_kv_heads);
@@ -852,7 +893,7 @@ __global__ __launch_bounds__(256) void prefill_merge_kernel(PrefillParams p) {
     lj_raw[r] = l < splits ? p.partial_ml[pr * 2 + 1] : 0.f;
 #pragma unroll
     for (int j = 0; j < kMaxSplits; j++) {
-      const float* src = p.partial_o + (prow0 + (int64_t)j * kBlockRows + r) * D + l * kPer;
+      const float* src = p.partial_o + (prow0 + (int64_t)j * kBlockRows + r) * D + ld * kPer;
 #pragma unroll
       for (int e = 0; e < kPer; e++) v[r][j][e] = j < splits ? src[e] : 0.f;
     }
@@ -891,25 +932,24 @@ __global__ __launch_bounds__(256) void prefill_merge_kernel(PrefillParams p) {
     const float inv = 1.f / den;
     if (p.state_o) {
       const int64_t srow = (int64_t)(h * p.group_size + qr) * p.state_tokens + s.q_start + i;
+      if (kDimLanes == 64 || l < kDimLanes) {
 #pragma unroll
-      for (int e = 0; e < kPer; e++) p.state_o[srow * D + l * kPer + e] = acc[e] * inv;
+        for (int e = 0; e < kPer; e++) p.state_o[srow * D + ld * kPer + e] = acc[e] * inv;
+      }
       if (l == 0) p.state_lse[srow] = m_use + __log2f(den);
       continue;
     }
+    if (kDimLanes < 64 && l >= kDimLanes) continue;
     T* dst = static_cast<T*>(p.out) + (int64_t)(h * p.group_size + qr) * p.out_stride_head +
-             (int64_t)(s.q_start + i) * p.out_stride_token + l * kPer;
+             (int64_t)(s.q_start + i) * p.out_stride_token + ld * kPer;
 #pragma unroll
     for (int e = 0; e < kPer; e++) dst[e] = (T)(acc[e] * inv);
   }
 }
 
-// Key tile per group and step: 64 tokens for F16 (the per-tile row max,
-// rescale test, barrier and block-table work spread over twice the keys:
-// 48.8 -> 47.0 us on the Qwen2-7B chunk, 32.3 -> 31.5 us on a Qwen2-0.5B-shape
-// chunk), 32 for F32, whose 64-token stages would not fit in LDS.
 template <int D, typename T>
 hipError_t launch_typed(const PrefillParams& params, hipStream_t stream) {
-  constexpr int TT = sizeof(T) == 4 ? 32 : 64;
+  constexpr int TT = prefill_tile_tokens<D, T>();
   const int64_t blocks = prefill_main_blocks(params) + params.catch_count;
   hipLaunchKernelGGL((paged_prefill_kernel<D, T>), dim3((unsigned)blocks), dim3(kWaves * 64), 0, stream, params);
   hipError_t err = hipGetLastError();
@@ -924,12 +964,16 @@ hipError_t launch_typed(const PrefillParams& params, hipStream_t stream) {
 } // namespace
 
 hipError_t launch_paged_prefill(const PrefillParams& params, int head_dim, bool f32, hipStream_t stream) {
+  if (!prefill_head_dim_supported(head_dim, f32)) return hipErrorInvalidValue;
   if (f32) {
     if (head_dim == 128) return launch_typed<128, float>(params, stream);
     if (head_dim == 64) return launch_typed<64, float>(params, stream);
+    if (head_dim == 32) return launch_typed<32, float>(params, stream);
   } else {
     if (head_dim == 128) return launch_typed<128, half_t>(params, stream);
     if (head_dim == 64) return launch_typed<64, half_t>(params, stream);
+    if (head_dim == 32) return launch_typed<32, half_t>(params, stream);
+    if (head_dim == 96) return launch_typed<96, half_t>(params, stream);
   }
   return hipErrorInvalidValue;
 }

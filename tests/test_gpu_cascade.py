@@ -144,17 +144,18 @@ def test_ragged_groups_match_oracle(dtype, d):
     check(w, vals, got, f"ragged groups {dtype} D={d}")
 
 
-def test_prefix_pass_on_the_prefill_kernel():
+@pytest.mark.parametrize("d", [128, 96])
+def test_prefix_pass_on_the_prefill_kernel(d):
     # 2 x 40 query tokens x 4 heads per KV head = 320 rows share a 512-token prefix: the prefix pass is a dense
     # contraction and takes the chunked-prefill kernel; the suffix pass stays on the split-context kernel.
     q_lens = [40, 40, 3]
     cached = [600, 512, 900]
     groups = [(0, 2, 512)]
-    w = shared_prefix_workload("f16", 128, 16, q_lens, cached, groups, hq=16, hkv=4, seed=9)
+    w = shared_prefix_workload("f16", d, 16, q_lens, cached, groups, hq=16, hkv=4, seed=9)
     vals = W.host_values(w)
     t = W.device_tensors(w, vals)
     got = run_cascade(w, t, groups, [512, 512, 0])
-    check(w, vals, got, "prefill-kernel prefix pass")
+    check(w, vals, got, f"prefill-kernel prefix pass D={d}")
 
 
 def test_no_groups_equals_plain_call():

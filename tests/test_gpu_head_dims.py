@@ -2,11 +2,13 @@
 
 The reference's attention takes any head dimension (AttentionDimensions, common.rs:189-206); its own Qwen2 and
 Llama shapes use 64 and 128, which keep every plan.  The others run the split-context kernel with 16-row tiles in
-1-wavefront blocks and the merge pass, so each is checked on the call shapes that reach different parts of it:
-a ragged decode batch (partials merged across partitions), verification rows (two row tiles per KV head), a
-prefill-sized call (many row tiles, causal limits inside the query), a mixed batch in 5-token pages (the repack
-into 16-token pages, with host hints), and one long context (more than 64 partitions: the merge's wide rounds).
-Output starts as NaN and must be finite everywhere and within 2e-3 (F16) / 1e-5 (F32) of the oracle.
+1-wavefront blocks and the merge pass, and prefill-sized calls at F16 32 and 96 and F32 32 the prefill kernel, so
+each is checked on the call shapes that reach different parts of them: a ragged decode batch (partials merged
+across partitions), verification rows (two row tiles per KV head), a prefill-sized call (many row tiles, causal
+limits inside the query), a mixed batch in 5-token pages (the repack into 16-token pages, with host hints), one
+long context (more than 64 partitions: the merge's wide rounds) and a chunk on a long context (the prefill
+kernel's key splits and their merge).  Output starts as NaN and must be finite everywhere and within 2e-3 (F16) /
+1e-5 (F32) of the oracle.
 """
 import math
 import sys
@@ -31,6 +33,7 @@ CASES = {
     "prefill": ([40, 70], [100, 300], 16, "cu"),
     "mixed-repacked": ([1, 1, 37, 1], [500, 20, 100, 900], 5, "both"),
     "long-context": ([1], [19999], 16, "none"),
+    "prefill-key-splits": ([64], [8000], 32, "none"),
 }
 
 
