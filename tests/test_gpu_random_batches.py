@@ -4,11 +4,12 @@ follow from the batch's shape, so a sweep over shapes reaches combinations that 
 
 Each case draws: F16 or F32; (Hq, Hkv, D) from the shapes of the reference's target and draft models
 (Qwen2.5-0.5B 14/2/64, Qwen2.5-1.5B 12/2/128, Qwen2.5-7B 28/4/128, Llama-3.2-1B 32/8/64, Llama-3.2-3B
-24/8/128, Llama-3.1-8B 32/8/128) and two others (8/8/64, 16/2/128); 1-80 sequences; per sequence a cached length
-and a query length (decodes, verification rows, prefill chunks, in any order); a page size from 1 to 48; and
-how the host hints are passed (none, both tables, only cu_q_lens, stale copies).  The output starts as NaN and
-must be finite everywhere and within 2e-3 (F16) / 1e-5 (F32) of the oracle.  Sizes stay small enough for the
-oracle to run in well under a second per case.
+24/8/128, Llama-3.1-8B 32/8/128) and five others (8/8/64, 16/2/128, and the head dimensions 96, 32 and 256 as
+16/2/96, 12/4/32 and 8/4/256); 1-80 sequences; per sequence a cached length and a query length (decodes,
+verification rows, prefill chunks, in any order); a page size from 1 to 48; and how the host hints are passed
+(none, both tables, only cu_q_lens, stale copies).  The output starts as NaN and must be finite everywhere and
+within 2e-3 (F16) / 1e-5 (F32) of the oracle.  Sizes stay small enough for the oracle to run in well under a
+second per case.
 """
 import math
 import sys
@@ -25,7 +26,8 @@ import workloads as W  # noqa: E402
 pytestmark = pytest.mark.gpu
 
 TOL = {"f32": 1e-5, "f16": 2e-3}
-SHAPES = [(14, 2, 64), (12, 2, 128), (28, 4, 128), (32, 8, 64), (24, 8, 128), (32, 8, 128), (8, 8, 64), (16, 2, 128)]
+SHAPES = [(14, 2, 64), (12, 2, 128), (28, 4, 128), (32, 8, 64), (24, 8, 128), (32, 8, 128), (8, 8, 64), (16, 2, 128),
+          (16, 2, 96), (12, 4, 32), (8, 4, 256)]
 PAGES = [1, 2, 3, 5, 8, 16, 16, 16, 24, 32, 48]
 HINTS = ["none", "both", "cu", "stale"]
 N_CASES = 96
