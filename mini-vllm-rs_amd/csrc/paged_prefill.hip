@@ -481,13 +481,22 @@ __device__ __forceinline__ void prefill_tile_serial(const PrefillParams& p, cons
     }
     lsum += psum;
   };
-  typedef float vrow_t __attribute__((ext_vector_type(D / 32)));
+  // A lane's D/32 consecutive elements of a row: one vector access where that
+  // is 1, 2 or 4 elements, one access per element otherwise (D = 96).
+  constexpr bool kVecRow = D / 32 == 1 || D / 32 == 2 || D / 32 == 4;
+  typedef float vrow_t __attribute__((ext_vector_type(kVecRow ? D / 32 : 1)));
   auto pv32 = [&](const T* vb, const float16v& pe) {
 #pragma unroll
     for (int e = 0; e < 16; e++) {
-      const vrow_t vf = *reinterpret_cast<const vrow_t*>(vb + rv[0] + (8 * (e >> 2) + (e & 3)) * D);
+      const T* src = vb + rv[0] + (8 * (e >> 2) + (e & 3)) * D;
+      if constexpr (kVecRow) {
+        const vrow_t vf = *reinterpret_cast<const vrow_t*>(src);
 #pragma unroll
-      for (int n = 0; n < D / 32; n++) o[n] = __builtin_amdgcn_mfma_f32_32x32x2f32(vf[n], pe[e], o[n], 0, 0, 0);
+        for (int n = 0; n < D / 32; n++) o[n] = __builtin_amdgcn_mfma_f32_32x32x2f32(vf[n], pe[e], o[n], 0, 0, 0);
+      } else {
+#pragma unroll
+        for (int n = 0; n < D / 32; n++) o[n] = __builtin_amdgcn_mfma_f32_32x32x2f32(src[n], pe[e], o[n], 0, 0, 0);
+      }
     }
   };
 
@@ -645,10 +654,16 @@ __device__ __forceinline__ void prefill_tile_serial(const PrefillParams& p, cons
     auto put = [&](float* dst, float scale) {
 #pragma unroll
       for (int e = 0; e < 16; e++) {
-        vrow_t v;
+        float* row = dst + (D / 32) * (8 * (e >> 2) + 4 * hh + (e & 3));
+        if constexpr (kVecRow) {
+          vrow_t v;
 #pragma unroll
-        for (int n = 0; n < D / 32; n++) v[n] = o[n][e] * scale;
-        *reinterpret_cast<vrow_t*>(dst + (D / 32) * (8 * (e >> 2) + 4 * hh + (e & 3))) = v;
+          for (int n = 0; n < D / 32; n++) v[n] = o[n][e] * scale;
+          *reinterpret_cast<vrow_t*>(row) = v;
+        } else {
+#pragma unroll
+          for (int n = 0; n < D / 32; n++) row[n] = o[n][e] * scale;
+        }
       }
     };
     if (!valid) return;
@@ -969,6 +984,7 @@ hipError_t launch_paged_prefill(const PrefillParams& params, int head_dim, bool 
     if (head_dim == 128) return launch_typed<128, float>(params, stream);
     if (head_dim == 64) return launch_typed<64, float>(params, stream);
     if (head_dim == 32) return launch_typed<32, float>(params, stream);
+    if (head_dim == 96) return launch_typed<96, float>(params, stream);
   } else {
     if (head_dim == 128) return launch_typed<128, half_t>(params, stream);
     if (head_dim == 64) return launch_typed<64, half_t>(params, stream);
