@@ -81,8 +81,7 @@ typedef struct mvr_paged_attention_args {
   int32_t num_q_heads;
   int32_t num_kv_heads;      /* divides num_q_heads */
   int32_t head_dim;          /* a multiple of 32 in [32, 256]; 64 and 128 take every plan, the others the
-                                split-context kernel with its merge pass (and, at 32 and 96,
-                                the chunked-prefill kernel for prefill-sized calls) */
+                                split-context kernel with its merge pass and the chunked-prefill kernel */
   int32_t page_size;         /* per_page_token_count, any positive value; sizes that are not a multiple of
                                 16 are read in place by decode-sized calls (2 tokens or more), and
                                 repacked into 16-token pages in the workspace first by prefill-sized calls

@@ -51,9 +51,15 @@ typedef __attribute__((address_space(4))) int32_t const_i32;
 
 constexpr int kRowsPerWave = 32;
 constexpr int kRowWaves = 4;                        // wavefronts per 128-row group
-constexpr int kGroups = 2;                          // wavefront groups taking alternating key tiles
-constexpr int kWaves = kRowWaves * kGroups;         // wavefronts per block
 constexpr int kBlockRows = kRowsPerWave * kRowWaves;
+// Groups of kRowWaves wavefronts per block, taking alternating key tiles: 2
+// (two wavefronts per SIMD), or 1 for rows of more than 128 elements, whose
+// state (O alone is D/2 registers per lane) needs the up to 512 registers of
+// one wavefront per SIMD.
+template <int D>
+constexpr int prefill_groups() {
+  return D > 128 ? 1 : 2;
+}
 constexpr int kMergeWaves = 4; // wavefronts per block of prefill_merge_kernel
 constexpr int kXcds = 8;
 #ifndef MVR_PREFILL_STAGES
@@ -142,14 +148,14 @@ __device__ __forceinline__ int block_key_tiles(const SeqRows& s, int group_size,
   return last_key < 0 ? 0 : last_key / TT + 1;
 }
 
-template <int D, typename T, int TT>
+template <int D, typename T, int TT, int G>
 struct Tile {
-  static constexpr int kSuperTokens = TT * kGroups; // tokens per LDS stage: one tile per group
+  static constexpr int kSuperTokens = TT * G; // tokens per LDS stage: one tile per group
   static constexpr bool kF32 = sizeof(T) == 4;
   static constexpr int kChunkElems = 16 / (int)sizeof(T);            // elements per 16-byte chunk
   static constexpr int kChunksPerRow = D / kChunkElems;              // 16-byte chunks per token row
   static constexpr int kChunks = kSuperTokens * kChunksPerRow;       // per K (or V) stage
-  static constexpr int kChunksPerThread = kChunks / (kWaves * 64);   // 4 at D=128, 2 at D=64 (F16 and F32)
+  static constexpr int kChunksPerThread = kChunks / (kRowWaves * G * 64); // D/32 (F16 and F32)
   static constexpr int kElems = kSuperTokens * D;
   // V: 32-byte pieces per row, XOR-swizzled with the row.  A transposed read
   // is served per half-wavefront: 4 rows x 2 adjacent pieces, which must land
@@ -175,10 +181,11 @@ struct Tile {
 
 // One (sequence, kv head, 128-row tile, key split): each step stages one
 // key tile per group, then QK^T, softmax and PV in turn.
-template <int D, typename T, int TT>
+template <int D, typename T, int TT, int G>
 __device__ __forceinline__ void prefill_tile_serial(const PrefillParams& p, const SeqRows& s, int b, int h, int rt,
                                                     int split, int kv_splits) {
-  typedef Tile<D, T, TT> TL;
+  static_assert(G == 1 || G == 2, "one or two wavefront groups");
+  typedef Tile<D, T, TT, G> TL;
   constexpr bool kF32 = TL::kF32;
   // Key tile of one group per step: TT tokens = kSub S^T blocks of 32 tokens.
   constexpr int kTileTokens = TT;
@@ -203,7 +210,7 @@ __device__ __forceinline__ void prefill_tile_serial(const PrefillParams& p, cons
   const int l = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int rw = wave % kRowWaves;  // rows rw*32 .. +31 of the block
-  const int grp = wave / kRowWaves; // key tiles j0 + 2i + grp
+  const int grp = wave / kRowWaves; // key tiles j0 + G i + grp
   const int hh = l >> 5;            // lane half: 0 or 1
 
   const int rows = p.group_size * s.q_len;
@@ -295,19 +302,19 @@ __device__ __forceinline__ void prefill_tile_serial(const PrefillParams& p, cons
   // wait for lgkmcnt(0), which would also drain every LDS read in flight, so
   // the entries are fetched just before a barrier, where lgkmcnt is drained
   // anyway.
-  const int n_steps = (j1 - j0 + 1) / 2;
+  const int n_steps = (j1 - j0 + G - 1) / G;
   const int i_last = max(n_steps - 1, 0);
   struct Pages {
     int64_t pg;
   };
   auto fetch_pages = [&](int si) {
-    return Pages{bt[page_div(min((j0 + 2 * si) * kTileTokens + ld_t0, s.key_end - 1))]}; // wave-uniform
+    return Pages{bt[page_div(min((j0 + G * si) * kTileTokens + ld_t0, s.key_end - 1))]}; // wave-uniform
   };
   auto issue_stage = [&](int si, const Pages& pages, T* kb, T* vb) {
     // All wave-uniform: the wavefront's first token (the last key past the
     // end), its page row, and the bytes from there to the end of the page or
     // of the call's keys.
-    const int tc = min((j0 + 2 * si) * kTileTokens + ld_t0, s.key_end - 1);
+    const int tc = min((j0 + G * si) * kTileTokens + ld_t0, s.key_end - 1);
     const int row0 = page_mod(tc);
     const int64_t base = ((pages.pg * p.num_kv_heads + h) * p.page_size + row0) * D;
     const uint32_t bytes = (uint32_t)min(p.page_size - row0, s.key_end - tc) * D * (uint32_t)sizeof(T);
@@ -325,7 +332,7 @@ __device__ __forceinline__ void prefill_tile_serial(const PrefillParams& p, cons
   // wave rw in 1024 floats from float (n * 4 + rw) * 1024 of the stages'
   // concatenation, as float4 [e / 4][lane] (16-byte LDS accesses).
   constexpr int kStageFloats = TL::kElems * (int)sizeof(T) / 4;
-  static_assert((D / 32) * kRowWaves * 1024 <= 4 * kStageFloats, "O hand-off exceeds four stages");
+  static_assert(G == 1 || (D / 32) * kRowWaves * 1024 <= 4 * kStageFloats, "O hand-off exceeds four stages");
   auto xfer_o = [&](int n) -> float* {
     const int f = (n * kRowWaves + rw) * 1024;
     const int obj = f / kStageFloats;
@@ -392,12 +399,15 @@ __device__ __forceinline__ void prefill_tile_serial(const PrefillParams& p, cons
         for (int c = 0; c < 4; c++) acc[0] = __builtin_amdgcn_mfma_f32_32x32x2f32(kf[c], q[st][c], acc[0], 0, 0, 0);
       }
     } else {
+      // (Past the first 8 reads, rows of more than 128 elements: their
+      // chunks from the 17th on, +128 elements.)
 #pragma unroll
       for (int st = 0; st < D / 16; st++)
 #pragma unroll
         for (int c = 0; c < kSub; c++)
-          acc[c] = __builtin_amdgcn_mfma_f32_32x32x16_f16(*reinterpret_cast<const half8*>(kb + rkx[st] + 32 * c * D), q[st],
-                                                          acc[c], 0, 0, 0);
+          acc[c] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
+              *reinterpret_cast<const half8*>(kb + rkx[st % kKOffs] + (st / kKOffs) * 128 + 32 * c * D), q[st], acc[c],
+              0, 0, 0);
     }
   };
   // In block c the lane holds tokens tok0 + 32c + 8*(e/4) + 4*hh + e%4 of row rho.
@@ -551,7 +561,7 @@ __device__ __forceinline__ void prefill_tile_serial(const PrefillParams& p, cons
   auto step = [&](int si, auto st_c) {
     constexpr int st = decltype(st_c)::value;
     issue_stage(min(si + kAhead, i_last), next_pages, k_st[(st + kAhead) % kStages], v_st[(st + kAhead) % kStages]);
-    const int j = j0 + 2 * si + grp;
+    const int j = j0 + G * si + grp;
     if (visible(j)) {
       float16v sc[kSub];
       qk(k_st[st], rk, sc);
@@ -580,7 +590,7 @@ __device__ __forceinline__ void prefill_tile_serial(const PrefillParams& p, cons
   const int clear_tiles = min(j1, (block_min_limit + 1) / kTileTokens); // tiles j < this are clear
   // Clear steps (both tiles clear); their count is a multiple of kStages so
   // that the general loop starts on stage 0.
-  const int i_mid = max(0, (clear_tiles - j0) / 2) / kStages * kStages;
+  const int i_mid = max(0, (clear_tiles - j0) / G) / kStages * kStages;
 
   // Unrolled by kStages so that every stage is named statically: LDS
   // addresses become immediate offsets and each stage is its own object.
@@ -615,37 +625,39 @@ __device__ __forceinline__ void prefill_tile_serial(const PrefillParams& p, cons
 
   // Group 1 hands its running state to group 0, which merges:
   //   M = max(m0, m1), o = 2^(m0-M) o0 + 2^(m1-M) o1, l likewise.
-  if (grp == 1) {
+  if constexpr (G == 2) {
+    if (grp == 1) {
 #pragma unroll
-    for (int n = 0; n < D / 32; n++) {
-      float4v* dst = reinterpret_cast<float4v*>(xfer_o(n));
+      for (int n = 0; n < D / 32; n++) {
+        float4v* dst = reinterpret_cast<float4v*>(xfer_o(n));
 #pragma unroll
-      for (int e4 = 0; e4 < 4; e4++)
-        dst[e4 * 64 + l] = float4v{o[n][4 * e4], o[n][4 * e4 + 1], o[n][4 * e4 + 2], o[n][4 * e4 + 3]};
-    }
-    ml_xfer[rw][0][l] = m;
-    ml_xfer[rw][1][l] = lsum;
-  }
-  __syncthreads();
-  if (grp == 1) return;
-  {
-    const float m1 = ml_xfer[rw][0][l];
-    const float l1 = ml_xfer[rw][1][l];
-    const float mm = fmaxf(m, m1);
-    const float a0 = m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m - mm);
-    const float a1 = m1 == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m1 - mm);
-#pragma unroll
-    for (int n = 0; n < D / 32; n++) {
-      const float4v* src = reinterpret_cast<const float4v*>(xfer_o(n));
-#pragma unroll
-      for (int e4 = 0; e4 < 4; e4++) {
-        const float4v x = src[e4 * 64 + l];
-#pragma unroll
-        for (int c = 0; c < 4; c++) o[n][4 * e4 + c] = a0 * o[n][4 * e4 + c] + a1 * x[c];
+        for (int e4 = 0; e4 < 4; e4++)
+          dst[e4 * 64 + l] = float4v{o[n][4 * e4], o[n][4 * e4 + 1], o[n][4 * e4 + 2], o[n][4 * e4 + 3]};
       }
+      ml_xfer[rw][0][l] = m;
+      ml_xfer[rw][1][l] = lsum;
     }
-    lsum = a0 * lsum + a1 * l1;
-    m = mm;
+    __syncthreads();
+    if (grp == 1) return;
+    {
+      const float m1 = ml_xfer[rw][0][l];
+      const float l1 = ml_xfer[rw][1][l];
+      const float mm = fmaxf(m, m1);
+      const float a0 = m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m - mm);
+      const float a1 = m1 == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m1 - mm);
+#pragma unroll
+      for (int n = 0; n < D / 32; n++) {
+        const float4v* src = reinterpret_cast<const float4v*>(xfer_o(n));
+#pragma unroll
+        for (int e4 = 0; e4 < 4; e4++) {
+          const float4v x = src[e4 * 64 + l];
+#pragma unroll
+          for (int c = 0; c < 4; c++) o[n][4 * e4 + c] = a0 * o[n][4 * e4 + c] + a1 * x[c];
+        }
+      }
+      lsum = a0 * lsum + a1 * l1;
+      m = mm;
+    }
   }
 
   const float ltot = lsum + __shfl_xor(lsum, 32);
@@ -796,7 +808,7 @@ constexpr int prefill_tile_tokens() {
 template <int D, typename T>
 __device__ __forceinline__ void prefill_tile(const PrefillParams& p, const SeqRows& s, int b, int h, int rt, int split,
                                              int kv_splits) {
-  prefill_tile_serial<D, T, prefill_tile_tokens<D, T>()>(p, s, b, h, rt, split, kv_splits);
+  prefill_tile_serial<D, T, prefill_tile_tokens<D, T>(), prefill_groups<D>()>(p, s, b, h, rt, split, kv_splits);
 }
 
 __host__ __device__ __forceinline__ int64_t prefill_main_blocks(const PrefillParams& p) {
@@ -806,7 +818,7 @@ __host__ __device__ __forceinline__ int64_t prefill_main_blocks(const PrefillPar
 }
 
 template <int D, typename T>
-__global__ __launch_bounds__(kWaves * 64, 1) void paged_prefill_kernel(PrefillParams p) {
+__global__ __launch_bounds__(kRowWaves * prefill_groups<D>() * 64, 1) void paged_prefill_kernel(PrefillParams p) {
   const int x = blockIdx.x;
   const int main_seqs = p.seq_count ? p.seq_count : p.num_seqs;
   const int main_blocks = (int)prefill_main_blocks(p);
@@ -966,7 +978,8 @@ template <int D, typename T>
 hipError_t launch_typed(const PrefillParams& params, hipStream_t stream) {
   constexpr int TT = prefill_tile_tokens<D, T>();
   const int64_t blocks = prefill_main_blocks(params) + params.catch_count;
-  hipLaunchKernelGGL((paged_prefill_kernel<D, T>), dim3((unsigned)blocks), dim3(kWaves * 64), 0, stream, params);
+  hipLaunchKernelGGL((paged_prefill_kernel<D, T>), dim3((unsigned)blocks), dim3(kRowWaves * prefill_groups<D>() * 64), 0,
+                     stream, params);
   hipError_t err = hipGetLastError();
   if (err != hipSuccess || params.kv_splits == 1) return err;
   const int64_t split_pairs = (int64_t)(params.seq_count ? params.seq_count : params.num_seqs) * params.num_kv_heads;
@@ -985,11 +998,19 @@ hipError_t launch_paged_prefill(const PrefillParams& params, int head_dim, bool 
     if (head_dim == 64) return launch_typed<64, float>(params, stream);
     if (head_dim == 32) return launch_typed<32, float>(params, stream);
     if (head_dim == 96) return launch_typed<96, float>(params, stream);
+    if (head_dim == 160) return launch_typed<160, float>(params, stream);
+    if (head_dim == 192) return launch_typed<192, float>(params, stream);
+    if (head_dim == 224) return launch_typed<224, float>(params, stream);
+    if (head_dim == 256) return launch_typed<256, float>(params, stream);
   } else {
     if (head_dim == 128) return launch_typed<128, half_t>(params, stream);
     if (head_dim == 64) return launch_typed<64, half_t>(params, stream);
     if (head_dim == 32) return launch_typed<32, half_t>(params, stream);
     if (head_dim == 96) return launch_typed<96, half_t>(params, stream);
+    if (head_dim == 160) return launch_typed<160, half_t>(params, stream);
+    if (head_dim == 192) return launch_typed<192, half_t>(params, stream);
+    if (head_dim == 224) return launch_typed<224, half_t>(params, stream);
+    if (head_dim == 256) return launch_typed<256, half_t>(params, stream);
   }
   return hipErrorInvalidValue;
 }

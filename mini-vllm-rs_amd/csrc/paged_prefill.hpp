@@ -65,14 +65,12 @@ inline void page_divider(int32_t d, uint64_t& magic, int32_t& shift) {
   magic = (uint64_t)((((unsigned __int128)1 << shift) + (unsigned)d - 1) / (unsigned)d);
 }
 
-// Head dimensions the prefill kernel takes: 32, 64, 96 and 128 (F16 in
-// 64-token key tiles, F32 in 32-token tiles).  Wider rows exceed the 256
-// registers of two wavefronts per SIMD (F16 192 and 256 in 32-token tiles
-// spilled 48 and 284 bytes per lane), so those head dimensions run
-// prefill-sized calls on the split-context kernel.
+// Head dimensions the prefill kernel takes: every multiple of 32 up to 256
+// (F16 in 64-token key tiles, F32 in 32-token tiles; rows of more than 128
+// elements in blocks of one wavefront group, one wavefront per SIMD).
 constexpr bool prefill_head_dim_supported(int d, bool f32) {
   (void)f32;
-  return d == 32 || d == 64 || d == 96 || d == 128;
+  return d >= 32 && d <= 256 && d % 32 == 0;
 }
 
 // f32: F32 Q/K/V/out (v_mfma_f32_32x32x2_f32); otherwise F16.

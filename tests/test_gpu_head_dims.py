@@ -2,13 +2,13 @@
 
 The reference's attention takes any head dimension (AttentionDimensions, common.rs:189-206); its own Qwen2 and
 Llama shapes use 64 and 128, which keep every plan.  The others run the split-context kernel with 16-row tiles in
-1-wavefront blocks and the merge pass, and prefill-sized calls at 32 and 96 (F16 and F32) the prefill kernel, so
-each is checked on the call shapes that reach different parts of them: a ragged decode batch (partials merged
-across partitions), verification rows (two row tiles per KV head), a prefill-sized call (many row tiles, causal
-limits inside the query), a mixed batch in 5-token pages (the repack into 16-token pages, with host hints), one
-long context (more than 64 partitions: the merge's wide rounds) and a chunk on a long context (the prefill
-kernel's key splits and their merge).  Output starts as NaN and must be finite everywhere and within 2e-3 (F16) /
-1e-5 (F32) of the oracle.
+1-wavefront blocks and the merge pass, and prefill-sized calls the prefill kernel (rows of more than 128 elements
+in blocks of one wavefront group), so each is checked on the call shapes that reach different parts of them: a
+ragged decode batch (partials merged across partitions), verification rows (two row tiles per KV head), a
+prefill-sized call (causal limits inside the query), a mixed batch in 5-token pages (the repack into 16-token
+pages, with host hints), one long context (more than 64 partitions: the merge's wide rounds) and a chunk on a
+long context (the prefill kernel's key splits and their merge).  Output starts as NaN and must be finite
+everywhere and within 2e-3 (F16) / 1e-5 (F32) of the oracle.
 """
 import math
 import sys
