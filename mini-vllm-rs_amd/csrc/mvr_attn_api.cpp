@@ -214,14 +214,31 @@ mvr::PagedAttentionPlan make_plan(const mvr_paged_attention_args* a, bool allow_
     static const int split_override = env_int("MVR_ATTN_PREFILL_SPLITS", 0);
     int64_t splits = split_override;
     if (splits <= 0) {
-      // Split keys only while blocks leave CUs idle: one 4-wavefront block
-      // per CU ran faster than two half-length blocks plus the merge pass.
+      // Split keys only while blocks leave CUs idle: one block per CU ran
+      // faster than two half-length blocks plus the merge pass.
       splits = (int64_t)device_cus() / live_blocks;
       if (splits > key_tiles / 8) splits = key_tiles / 8; // keep >= 8 key tiles per split
     }
     if (splits > 8) splits = 8; // the merge holds one split per lane; 8 is plenty
     if (splits < 1) splits = 1;
     plan.kv_splits = (int)splits;
+    // Wavefront groups per block.  Two groups share a block's 128 rows and
+    // take alternating key tiles, two wavefronts per SIMD behind one barrier;
+    // rows of more than 128 elements take one group (one wavefront per SIMD
+    // holds their state).  F16 grids of at least 6 blocks per CU also take one
+    // group, two independent blocks per CU.  Measured on fresh prompts (F16,
+    // D=128), two groups -> one: Llama-3-8B 1 x 8192 589 -> 545 us, 4 x 2048
+    // 188 -> 164, Qwen2-7B 1 x 8192 518 -> 497, 1 x 16384 1880 -> 1818; on
+    // smaller grids one group lost up to 15% (the Qwen2-7B chunk, 224 blocks:
+    // 46.3 -> 53.0 us; Qwen2-7B 1 x 4096, 896 blocks: 151-160 -> 171).
+    // MVR_ATTN_PREFILL_GROUPS=1 or 2 forces a shape (2 only up to D=128).
+    static const int groups_override = env_int("MVR_ATTN_PREFILL_GROUPS", 0);
+    if (a->head_dim > 128)
+      plan.prefill_groups = 1;
+    else if (groups_override == 1 || groups_override == 2)
+      plan.prefill_groups = groups_override;
+    else
+      plan.prefill_groups = a->dtype == MVR_DTYPE_F16 && live_blocks * splits >= 6LL * device_cus() ? 1 : 2;
     if (splits > 1) {
       const int64_t split_seqs = live.split_count > 0 && live.split_count < a->num_seqs ? live.split_count : a->num_seqs;
       const size_t prow = (size_t)(split_seqs * a->num_kv_heads * plan.row_tiles) * splits * mvr::kPrefillBlockRows;
@@ -495,6 +512,7 @@ int launch_planned(const mvr_paged_attention_args* a, const mvr::PagedAttentionP
     mvr::page_divider(a->page_size, f.page_magic, f.page_magic_shift);
     f.row_tiles = plan.row_tiles;
     f.kv_splits = plan.kv_splits;
+    f.groups = plan.prefill_groups;
     f.scale_log2 = scale * 1.4426950408889634f;
     f.key_end = cp.key_end;
     f.state_o = cp.state_o;

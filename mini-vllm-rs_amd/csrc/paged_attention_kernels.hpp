@@ -81,6 +81,7 @@ struct PagedAttentionPlan {
   size_t partial_bytes; // workspace for partials (0 when max_parts == 1)
   bool prefill;         // chunked-prefill kernel (paged_prefill.hip) instead of the split-context one
   int kv_splits;        // prefill: key-range splits per 128-row tile
+  int prefill_groups;   // prefill: wavefront groups of 4 per block (2, or 1)
   bool block_merge;     // one block per tile, its partitions merged in LDS
   int block_waves;      // block_merge: wavefronts per block, 4, 8 or 16 (>= max_parts)
   bool dense_parts;     // ragged split plan: live units first, in a dense order (see dense_unit)

@@ -52,14 +52,12 @@ typedef __attribute__((address_space(4))) int32_t const_i32;
 constexpr int kRowsPerWave = 32;
 constexpr int kRowWaves = 4;                        // wavefronts per 128-row group
 constexpr int kBlockRows = kRowsPerWave * kRowWaves;
-// Groups of kRowWaves wavefronts per block, taking alternating key tiles: 2
-// (two wavefronts per SIMD), or 1 for rows of more than 128 elements, whose
-// state (O alone is D/2 registers per lane) needs the up to 512 registers of
-// one wavefront per SIMD.
-template <int D>
-constexpr int prefill_groups() {
-  return D > 128 ? 1 : 2;
-}
+// Groups of kRowWaves wavefronts per block, taking alternating key tiles
+// (PrefillParams::groups, chosen by the host): 2 (two wavefronts per SIMD
+// behind one barrier), or 1 (blocks of 4 wavefronts, two per CU up to D=128;
+// for rows of more than 128 elements always, whose state, O alone D/2
+// registers per lane, needs the up to 512 registers of one wavefront per
+// SIMD).
 constexpr int kMergeWaves = 4; // wavefronts per block of prefill_merge_kernel
 constexpr int kXcds = 8;
 #ifndef MVR_PREFILL_STAGES
@@ -805,10 +803,10 @@ constexpr int prefill_tile_tokens() {
 // one (sequence, kv head) pair sit on the same XCD, so their shared K/V stays
 // in that XCD's L2 (with fewer pairs than XCDs, plain linear order keeps
 // every XCD busy).  Catch-up blocks follow the main grid.
-template <int D, typename T>
+template <int D, typename T, int G>
 __device__ __forceinline__ void prefill_tile(const PrefillParams& p, const SeqRows& s, int b, int h, int rt, int split,
                                              int kv_splits) {
-  prefill_tile_serial<D, T, prefill_tile_tokens<D, T>(), prefill_groups<D>()>(p, s, b, h, rt, split, kv_splits);
+  prefill_tile_serial<D, T, prefill_tile_tokens<D, T>(), G>(p, s, b, h, rt, split, kv_splits);
 }
 
 __host__ __device__ __forceinline__ int64_t prefill_main_blocks(const PrefillParams& p) {
@@ -817,8 +815,8 @@ __host__ __device__ __forceinline__ int64_t prefill_main_blocks(const PrefillPar
   return pairs >= kXcds ? kXcds * ((pairs + kXcds - 1) / kXcds) * per_pair : pairs * per_pair;
 }
 
-template <int D, typename T>
-__global__ __launch_bounds__(kRowWaves * prefill_groups<D>() * 64, 1) void paged_prefill_kernel(PrefillParams p) {
+template <int D, typename T, int G>
+__global__ __launch_bounds__(kRowWaves* G * 64, (G == 1 && D <= 128) ? 2 : 1) void paged_prefill_kernel(PrefillParams p) {
   const int x = blockIdx.x;
   const int main_seqs = p.seq_count ? p.seq_count : p.num_seqs;
   const int main_blocks = (int)prefill_main_blocks(p);
@@ -830,7 +828,7 @@ __global__ __launch_bounds__(kRowWaves * prefill_groups<D>() * 64, 1) void paged
     if (s.q_len <= 0) return;
     for (int h = 0; h < p.num_kv_heads; h++)
       for (int rt = 0; rt < p.row_tiles; rt++) {
-        prefill_tile<D, T>(p, s, b, h, rt, 0, 1);
+        prefill_tile<D, T, G>(p, s, b, h, rt, 0, 1);
         __syncthreads(); // group 0's hand-off reads end before the next tile refills the stages
       }
     return;
@@ -872,7 +870,7 @@ __global__ __launch_bounds__(kRowWaves * prefill_groups<D>() * 64, 1) void paged
       rt = p.row_tiles - 1 - idx;
     }
   }
-  prefill_tile<D, T>(p, s, b, h, rt, split, p.kv_splits);
+  prefill_tile<D, T, G>(p, s, b, h, rt, split, p.kv_splits);
 }
 
 // Merges the kv_splits partial results of every block tile:
@@ -978,8 +976,17 @@ template <int D, typename T>
 hipError_t launch_typed(const PrefillParams& params, hipStream_t stream) {
   constexpr int TT = prefill_tile_tokens<D, T>();
   const int64_t blocks = prefill_main_blocks(params) + params.catch_count;
-  hipLaunchKernelGGL((paged_prefill_kernel<D, T>), dim3((unsigned)blocks), dim3(kRowWaves * prefill_groups<D>() * 64), 0,
-                     stream, params);
+  if constexpr (D > 128) {
+    if (params.groups != 1) return hipErrorInvalidValue;
+    hipLaunchKernelGGL((paged_prefill_kernel<D, T, 1>), dim3((unsigned)blocks), dim3(kRowWaves * 64), 0, stream, params);
+  } else if (params.groups == 1) {
+    hipLaunchKernelGGL((paged_prefill_kernel<D, T, 1>), dim3((unsigned)blocks), dim3(kRowWaves * 64), 0, stream, params);
+  } else if (params.groups == 2) {
+    hipLaunchKernelGGL((paged_prefill_kernel<D, T, 2>), dim3((unsigned)blocks), dim3(kRowWaves * 2 * 64), 0, stream,
+                       params);
+  } else {
+    return hipErrorInvalidValue;
+  }
   hipError_t err = hipGetLastError();
   if (err != hipSuccess || params.kv_splits == 1) return err;
   const int64_t split_pairs = (int64_t)(params.seq_count ? params.seq_count : params.num_seqs) * params.num_kv_heads;

@@ -50,6 +50,7 @@ struct PrefillParams {
   // (kv head, row tile) of its sequence unsplit (normally none has rows: they
   // cover sequences that host hints placed in another launch's class).
   int32_t catch_lo, catch_count;
+  int32_t groups; // wavefront groups of 4 per block: 2, or 1 (always 1 for head_dim > 128)
 };
 
 // Division by the invariant page_size as a multiply and a shift, the
