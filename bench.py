@@ -385,6 +385,48 @@ def measure_append(W, M, torch, cfg, steps, warmup):
     return res
 
 
+class GatherRunner:
+    """mvr_reconstruct_contiguous of one request's K: `tokens` tokens of the Llama-3-8B shape (8 KV heads, D 128) in
+    16-token pages in random order, into a preallocated [1, 8, tokens, 128] tensor."""
+
+    def __init__(self, torch, M, dtype, tokens):
+        import numpy as np
+        self.lib = M.load_library()
+        self.tokens = tokens
+        self.pages = (tokens + 15) // 16
+        tdt = torch.float16 if dtype == "f16" else torch.float32
+        self.pool = torch.randn((self.pages, 1, 8, 16, 128), dtype=tdt, device="cuda")
+        perm = np.random.default_rng(7).permutation(self.pages).astype(np.int32)
+        self.ids = torch.from_numpy(perm).cuda()
+        self.out = torch.empty((1, 8, tokens, 128), dtype=tdt, device="cuda")
+        self.code = M.dtype_code(self.pool)
+        self.stream = torch.cuda.current_stream().cuda_stream
+        self.bytes = 2 * self.out.numel() * self.out.element_size()
+
+    def step(self):
+        rc = self.lib.mvr_reconstruct_contiguous(self.code, self.pool.data_ptr(), self.pages, 8, 16, 128,
+                                                 self.ids.data_ptr(), self.pages, self.tokens, self.out.data_ptr(),
+                                                 self.stream)
+        assert rc == 0, rc
+
+
+def measure_gather(M, torch, steps, warmup):
+    """The gather-to-contiguous entry point on one request's K (read + written bytes)."""
+    res = {}
+    for dtype in ("f16", "f32"):
+        for tokens in (8192, 32768):
+            r = GatherRunner(torch, M, dtype, tokens)
+            _, per = time_steps(r, torch, steps, warmup)
+            med = per[len(per) // 2]
+            res[f"{dtype}/{tokens}"] = dict(
+                workload=f"reconstruct_contiguous of one {tokens}-token request's K, 8 KV heads, D 128, {dtype}",
+                us_per_step_median=round(med, 2), bytes=r.bytes, eff_gbs=round(r.bytes / (med * 1e-6) / 1e9, 1),
+                hbm_frac=round(r.bytes / (med * 1e-6) / 1e9 / HBM_PEAK_GBS, 4))
+            del r
+            torch.cuda.empty_cache()
+    return res
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -534,6 +576,8 @@ def main():
         for cfg in (3, 4):
             log(f"[bench] rope+append, config {cfg}")
             result["rope_append"][str(cfg)] = measure_append(W, M, torch, cfg, max(20, a.steps // 2), a.warmup)
+        log("[bench] gather to contiguous")
+        result["gather"] = measure_gather(M, torch, max(20, a.steps // 2), a.warmup)
     if not a.skip_cpu:
         log("[bench] cpu baseline")
         result["cpu_baseline"] = cpu_baseline(W)
