@@ -328,8 +328,11 @@ mvr::PagedAttentionPlan make_plan(const mvr_paged_attention_args* a, bool allow_
   // for head_dim 64 only.  MVR_ATTN_BLOCK_MERGE=false keeps the separate merge.
   static const bool block_merge_enabled = env_bool("MVR_ATTN_BLOCK_MERGE", true);
   plan.block_waves = 0;
-  if (block_merge_enabled && !ragged && plan.row_blocks == 1 && !plan.token_pages && all_plans) {
-    const int widest = a->dtype != MVR_DTYPE_F16 ? 4 : a->head_dim == 64 ? 16 : 8;
+  // Token pages take blocks of 4 or 8 wavefronts, and none in F32 at D=128
+  // (its registers would spill).
+  const bool bm_shape = !plan.token_pages || a->dtype == MVR_DTYPE_F16 || a->head_dim != 128;
+  if (block_merge_enabled && !ragged && plan.row_blocks == 1 && all_plans && bm_shape) {
+    const int widest = a->dtype != MVR_DTYPE_F16 ? 4 : a->head_dim == 64 && !plan.token_pages ? 16 : 8;
     for (int w = 4; w <= widest && plan.block_waves == 0; w *= 2)
       if (plan.max_parts <= w && 4 * plan.max_parts >= 3 * w) plan.block_waves = w;
   }

@@ -980,7 +980,21 @@ hipError_t launch_typed(const PagedAttentionPlan& plan, const PagedAttentionPara
       // One block of block_waves wavefronts per (sequence, KV head, row tile).
       const int64_t tiles = (int64_t)params.num_seqs * params.num_kv_heads * params.row_tiles;
       if (plan.max_parts > plan.block_waves || plan.num_units != tiles * plan.block_waves) return hipErrorInvalidValue;
-      if (plan.block_waves == 4) {
+      if (plan.token_pages) {
+        // Token pages: blocks of 4 or 8 wavefronts; not F32 at D=128, whose
+        // registers would spill.
+        if constexpr (sizeof(typename Tr::elem) == 4 && D == 128) {
+          return hipErrorInvalidValue;
+        } else if (plan.block_waves == 4) {
+          hipLaunchKernelGGL((paged_attention_kernel<Tr, D, NB, true, false, 2, 4, true>), dim3((unsigned)tiles),
+                             dim3(kWaveSize * 4), 0, stream, params);
+        } else if (plan.block_waves == 8) {
+          hipLaunchKernelGGL((paged_attention_kernel<Tr, D, NB, true, false, 2, 8, true>), dim3((unsigned)tiles),
+                             dim3(kWaveSize * 8), 0, stream, params);
+        } else {
+          return hipErrorInvalidValue;
+        }
+      } else if (plan.block_waves == 4) {
         hipLaunchKernelGGL((paged_attention_kernel<Tr, D, NB, true, false, 2, 4>), dim3((unsigned)tiles),
                            dim3(kWaveSize * 4), 0, stream, params);
       } else if (plan.block_waves == 8) {
