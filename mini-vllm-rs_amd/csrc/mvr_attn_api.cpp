@@ -206,7 +206,7 @@ mvr::PagedAttentionPlan make_plan(const mvr_paged_attention_args* a, bool allow_
   // kernel serves, which then reads them in place (token pages).
   plan.token_pages = !page_runs;
   if (allow_prefill && prefill_enabled && (rows_max > 64 || force_prefill) && page_runs &&
-      mvr::prefill_head_dim_supported(a->head_dim, a->dtype == MVR_DTYPE_F32)) {
+      mvr::prefill_head_dim_supported(a->head_dim)) {
     plan.prefill = true;
     plan.row_tiles = (int)((rows_max + mvr::kPrefillBlockRows - 1) / mvr::kPrefillBlockRows);
     const int64_t live_blocks = n_live * a->num_kv_heads * plan.row_tiles;

@@ -999,7 +999,7 @@ hipError_t launch_typed(const PrefillParams& params, hipStream_t stream) {
 } // namespace
 
 hipError_t launch_paged_prefill(const PrefillParams& params, int head_dim, bool f32, hipStream_t stream) {
-  if (!prefill_head_dim_supported(head_dim, f32)) return hipErrorInvalidValue;
+  if (!prefill_head_dim_supported(head_dim)) return hipErrorInvalidValue;
   if (f32) {
     if (head_dim == 128) return launch_typed<128, float>(params, stream);
     if (head_dim == 64) return launch_typed<64, float>(params, stream);

@@ -69,10 +69,7 @@ inline void page_divider(int32_t d, uint64_t& magic, int32_t& shift) {
 // Head dimensions the prefill kernel takes: every multiple of 32 up to 256
 // (F16 in 64-token key tiles, F32 in 32-token tiles; rows of more than 128
 // elements in blocks of one wavefront group, one wavefront per SIMD).
-constexpr bool prefill_head_dim_supported(int d, bool f32) {
-  (void)f32;
-  return d >= 32 && d <= 256 && d % 32 == 0;
-}
+constexpr bool prefill_head_dim_supported(int d) { return d >= 32 && d <= 256 && d % 32 == 0; }
 
 // f32: F32 Q/K/V/out (v_mfma_f32_32x32x2_f32); otherwise F16.
 hipError_t launch_paged_prefill(const PrefillParams& params, int head_dim, bool f32, hipStream_t stream);
