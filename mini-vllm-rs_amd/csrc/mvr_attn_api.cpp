@@ -225,12 +225,14 @@ mvr::PagedAttentionPlan make_plan(const mvr_paged_attention_args* a, bool allow_
     // Wavefront groups per block.  Two groups share a block's 128 rows and
     // take alternating key tiles, two wavefronts per SIMD behind one barrier;
     // rows of more than 128 elements take one group (one wavefront per SIMD
-    // holds their state).  F16 grids of at least 6 blocks per CU also take one
+    // holds their state).  F16 grids of at least 4 blocks per CU also take one
     // group, two independent blocks per CU.  Measured on fresh prompts (F16,
     // D=128), two groups -> one: Llama-3-8B 1 x 8192 589 -> 545 us, 4 x 2048
-    // 188 -> 164, Qwen2-7B 1 x 8192 518 -> 497, 1 x 16384 1880 -> 1818; on
-    // smaller grids one group lost up to 15% (the Qwen2-7B chunk, 224 blocks:
-    // 46.3 -> 53.0 us; Qwen2-7B 1 x 4096, 896 blocks: 151-160 -> 171).
+    // 188 -> 164, 1 x 4096 (1,024 blocks) 184-201 -> 172-184, Qwen2-7B 1 x
+    // 8192 518 -> 497, 1 x 16384 1880 -> 1818; on smaller grids one group lost
+    // up to 15% (the Qwen2-7B chunk, 224 blocks: 46.3 -> 53.0 us; Qwen2-7B 1 x
+    // 4096, 896 blocks: 151-164 -> 171-178).  (One group in 32-token key tiles
+    // instead of 64: 3-8% slower on these prompts.)
     // MVR_ATTN_PREFILL_GROUPS=1 or 2 forces a shape (2 only up to D=128).
     static const int groups_override = env_int("MVR_ATTN_PREFILL_GROUPS", 0);
     if (a->head_dim > 128)
@@ -238,7 +240,7 @@ mvr::PagedAttentionPlan make_plan(const mvr_paged_attention_args* a, bool allow_
     else if (groups_override == 1 || groups_override == 2)
       plan.prefill_groups = groups_override;
     else
-      plan.prefill_groups = a->dtype == MVR_DTYPE_F16 && live_blocks * splits >= 6LL * device_cus() ? 1 : 2;
+      plan.prefill_groups = a->dtype == MVR_DTYPE_F16 && live_blocks * splits >= 4LL * device_cus() ? 1 : 2;
     if (splits > 1) {
       const int64_t split_seqs = live.split_count > 0 && live.split_count < a->num_seqs ? live.split_count : a->num_seqs;
       const size_t prow = (size_t)(split_seqs * a->num_kv_heads * plan.row_tiles) * splits * mvr::kPrefillBlockRows;

@@ -2,7 +2,7 @@
 
 Up to D=128 a prefill block holds 128 grouped rows either in two groups of 4 wavefronts that take alternating
 key tiles and merge at the end (two wavefronts per SIMD behind one barrier), or in one group of 4 wavefronts that
-steps through every key tile (two such blocks per CU).  The planner takes one group for F16 grids of at least 6
+steps through every key tile (two such blocks per CU).  The planner takes one group for F16 grids of at least 4
 blocks per CU and two otherwise; MVR_ATTN_PREFILL_GROUPS forces either (read once per process, so each shape runs
 in a child process).  Both must meet the same bar against the oracle: 2e-3 (F16) / 1e-5 (F32).  Cases: the
 Qwen2-7B chunk in F16 and F32, ragged chunks on long contexts at D=64 (key splits and their merge), and a mixed
