@@ -7,14 +7,16 @@
 // contraction (about 950 flop per byte of K/V at q_len 256) and the MFMA
 // pipes, not HBM, set the roofline.
 //
-// Block = 8 wavefronts over 128 consecutive grouped rows of one (sequence, KV
-// head): two groups of 4 wavefronts (32 rows each) hold the same rows and
-// take alternating key tiles (TT = 64 tokens for F16, 32 for F32), so every
-// SIMD runs two wavefronts without splitting the keys across blocks; at the
-// end group 1 hands its (O, m, l) to group 0 through LDS and group 0 merges
-// and writes.  Each step stages 2 TT tokens (one tile per group) in LDS
+// Block = G groups of 4 wavefronts over 128 consecutive grouped rows of one
+// (sequence, KV head), 32 rows per wavefront.  G = 2: the two groups hold the
+// same rows and take alternating key tiles (TT = 64 tokens for F16, 32 for
+// F32), so every SIMD runs two wavefronts without splitting the keys across
+// blocks; at the end group 1 hands its (O, m, l) to group 0 through LDS and
+// group 0 merges and writes.  G = 1 (large F16 grids, two blocks per CU; rows
+// of more than 128 elements, one wavefront per SIMD): one group steps through
+// every key tile.  Each step stages G TT tokens (one tile per group) in LDS
 // through a ring of kStages stages filled by direct-to-LDS loads (32 KiB of K
-// and of V per stage at D=128 F16):
+// and of V per stage at D=128 F16, G = 2):
 //   * K tile: 16-byte chunks, XOR swizzle (chunk ^ row%16), read back with
 //     ds_read_b128 in the v_mfma_f32_32x32x16_f16 A-operand layout
 //     (lane l: token l%32, dims 8*(l/32)+16s);  S^T = K Q^T in D/16 MFMAs
