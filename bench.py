@@ -443,6 +443,8 @@ def main():
     ap.add_argument("--decode-map", action="store_true",
                     help="time only ragged against uniform decode batches of about equal bytes (Llama-3-8B, F16)")
     ap.add_argument("--f32", action="store_true", help="with --only-config 4: the same chunked prefill in F32")
+    ap.add_argument("--only-fresh", action="store_true",
+                    help="time only the Qwen2-7B fresh 8,192-token prompt (F16 prefill, one call)")
     ap.add_argument("--head-dims", action="store_true",
                     help="time only the headline decode shape at every supported head dimension")
     a = ap.parse_args()
@@ -472,6 +474,11 @@ def main():
         return
     if a.head_dims:
         print(json.dumps({"head_dims": measure_head_dims(W, M, torch, a.steps, a.warmup)}), flush=True)
+        return
+    if a.only_fresh:
+        log("[bench] Qwen2-7B fresh 8,192-token prompt only")
+        res = measure(W, M, torch, lambda: W.fresh_prompt_f16("qwen2-7b", 8192), a.steps, a.warmup)
+        print(json.dumps({"fresh_prompt": {"qwen2-7b 1x8192": res}, "steps": a.steps, "warmup": a.warmup}), flush=True)
         return
     if a.f32 and a.only_config != 4:
         print("--f32 goes with --only-config 4", file=sys.stderr)
