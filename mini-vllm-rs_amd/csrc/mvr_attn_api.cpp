@@ -192,8 +192,9 @@ mvr::PagedAttentionPlan make_plan(const mvr_paged_attention_args* a, bool allow_
   const int group = a->num_q_heads / a->num_kv_heads;
   const int64_t rows_max = (int64_t)group * a->max_q_len;
   // Head dimensions other than 64 and 128: the split-context kernel in its
-  // plain form (16-row tiles, 1-wavefront blocks, the merge pass), and the
-  // prefill kernel where it takes them.
+  // plain form (16-row tiles, 1-wavefront blocks, the merge pass) for
+  // decode-sized calls; prefill-sized calls take the prefill kernel as at 64
+  // and 128.
   const bool all_plans = mvr::head_dim_all_plans(a->head_dim);
   // Many query rows per KV head (chunked prefill): dense contraction, use the
   // LDS-shared 32x32 MFMA kernel (F16 32x32x16, F32 32x32x2).
