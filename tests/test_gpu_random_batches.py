@@ -30,7 +30,7 @@ SHAPES = [(14, 2, 64), (12, 2, 128), (28, 4, 128), (32, 8, 64), (24, 8, 128), (3
           (16, 2, 96), (12, 4, 32), (8, 4, 256)]
 PAGES = [1, 2, 3, 5, 8, 16, 16, 16, 24, 32, 48]
 HINTS = ["none", "both", "cu", "stale"]
-N_CASES = 96
+N_CASES = 200
 
 
 def say(msg):
