@@ -265,13 +265,13 @@ __device__ __forceinline__ void prefill_tile_serial(const PrefillParams& p, cons
   auto page_div = [&](int tok) { return (int)(((uint64_t)(uint32_t)tok * p.page_magic) >> p.page_magic_shift); };
   auto page_mod = [&](int tok) { return tok - page_div(tok) * p.page_size; };
 
-  // A stage holds the 2 TT tokens of one step: tile j0 + 2i (group 0) in rows
-  // 0..TT-1 and tile j0 + 2i + 1 (group 1) in rows TT..2TT-1.  Tokens move
-  // straight from HBM/L2 into LDS (buffer_load_dwordx4 ... lds: lane i of a
-  // wavefront writes 16 bytes at the wavefront's LDS base + 16 i), so they
-  // take no registers and no LDS store instructions.  Wavefront w fills the
-  // stage's rows w*R .. w*R+R-1 (R = 2 TT / 8 tokens: 16 for F16, 8 for F32),
-  // its load u LDS chunks (w*kChunksPerThread + u)*64 .. +63; LDS chunk P
+  // A stage holds the G TT tokens of one step: tile j0 + G i + g (group g) in
+  // rows g TT .. g TT + TT - 1.  Tokens move straight from HBM/L2 into LDS
+  // (buffer_load_dwordx4 ... lds: lane i of a wavefront writes 16 bytes at the
+  // wavefront's LDS base + 16 i), so they take no registers and no LDS store
+  // instructions.  Wavefront w fills the stage's rows w*R .. w*R+R-1 (R = G TT
+  // / (4 G) tokens: 16 for F16, 8 for F32), its load u LDS chunks
+  // (w*kChunksPerThread + u)*64 .. +63; LDS chunk P
   // holds token row t = P / (D/8), physical chunk P % (D/8), and the lane
   // fetches the logical 16-byte chunk that the K or V swizzle puts there.  A
   // wavefront's R tokens are consecutive and start at a multiple of R, hence
