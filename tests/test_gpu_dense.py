@@ -6,8 +6,10 @@ lets each wavefront find its unit with a wave-wide scan of the sequence
 lengths (dense_unit).  Same bar as every call: 2e-3 (F16) / 1e-5 (F32)
 against the oracle.  Covers 64 sequences of 257..2049 tokens (F16, D=128), 150
 sequences of 17..1024 tokens (more than one 64-sequence block of the scan, the
-F16 D=64 kernel) and 40 F32 sequences at D=64 and at D=128 (whose key rows
-of 512 bytes take the finer dense split).  By default a dense plan also splits
+F16 D=64 kernel), 40 F32 sequences at D=64 and at D=128 (whose key rows
+of 512 bytes take the finer dense split), and, for contrast, two such batches
+in pages of 8 and 5 tokens read in place (token pages), which keep the
+slot == partition layout.  By default a dense plan also splits
 contexts into more partitions than the slot == partition plan of the same
 batch (a higher fill target), which changes the rounding.  With the same
 partitions the dense layout only changes which wavefront computes which
@@ -50,12 +52,12 @@ def _gpu():
     O.build()
 
 
-def ragged_workload(name, dtype, hq, hkv, d, n, lo, hi, seed):
+def ragged_workload(name, dtype, hq, hkv, d, n, lo, hi, seed, page=16):
     rng = np.random.default_rng(seed)
     seq_lens = rng.integers(lo, hi, size=n, endpoint=True).astype(np.int32)
-    pages = int(sum((int(L) + 15) // 16 for L in seq_lens)) + 8
-    bt = W._assign_pages(rng, seq_lens, 16, pages)
-    return W.Workload(name, dtype, hq, hkv, d, 16, pages, 0.3, seq_lens, np.ones(n, np.int32), bt, seed)
+    pages = int(sum((int(L) + page - 1) // page for L in seq_lens)) + 8
+    bt = W._assign_pages(rng, seq_lens, page, pages)
+    return W.Workload(name, dtype, hq, hkv, d, page, pages, 0.3, seq_lens, np.ones(n, np.int32), bt, seed)
 
 
 CASES = {
@@ -63,6 +65,9 @@ CASES = {
     "f16-d64-150x[17,1024]": ("f16", 14, 2, 64, 150, 17, 1024, 72),
     "f32-d64-40x[100,3000]": ("f32", 14, 2, 64, 40, 100, 3000, 73),
     "f32-d128-40x[512,4096]": ("f32", 32, 8, 128, 40, 512, 4096, 74),
+    # pages of 8 and 5 tokens, read in place (token pages); such batches keep the slot == partition layout
+    "f16-d128-64x[257,2049]-p8": ("f16", 32, 8, 128, 64, 257, 2049, 75, 8),
+    "f32-d64-40x[100,3000]-p5": ("f32", 14, 2, 64, 40, 100, 3000, 76, 5),
 }
 
 
