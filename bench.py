@@ -320,10 +320,11 @@ def measure_mixed(W, M, torch, steps, warmup):
 
 def measure_page_sizes(W, M, torch, steps, warmup):
     """Configs 3 and 4 in pages of other sizes (README.md:175-176 lets the runner pick any): multiples of 16
-    are read in place, other sizes repacked into 16-token pages in the workspace first (a K/V copy inside every
-    call)."""
+    are read in place, and so are 8- and 5-token pages by the decode call and 8-token pages by the prefill
+    call; the prefill call repacks 5-token pages into 16-token pages in the workspace first (a K/V copy
+    inside every call)."""
     res = {}
-    for cfg, sizes in ((3, (32, 48, 8, 5)), (4, (48, 8))):
+    for cfg, sizes in ((3, (32, 48, 8, 5)), (4, (48, 8, 5))):
         for ps in sizes:
             log(f"[bench] config {cfg} in {ps}-token pages")
             res[f"{cfg}/{ps}"] = measure(W, M, torch, lambda: W.repaged(W.CONFIGS[cfg](), ps), steps, warmup)

@@ -83,9 +83,11 @@ typedef struct mvr_paged_attention_args {
   int32_t head_dim;          /* a multiple of 32 in [32, 256]; 64 and 128 take every plan, the others the
                                 split-context kernel with its merge pass and the chunked-prefill kernel */
   int32_t page_size;         /* per_page_token_count, any positive value; sizes that are not a multiple of
-                                16 are read in place by decode-sized calls (2 tokens or more), and
-                                repacked into 16-token pages in the workspace first by prefill-sized calls
-                                and for 1-token pages */
+                                16 are read in place by decode-sized calls (2 tokens or more) and, at
+                                head_dim 64 and 128, by prefill-sized calls whose page size is a multiple
+                                of the tokens one prefill load covers (F16: 4 at D=128, 8 at D=64; F32: 2
+                                at D=128, 4 at D=64); the others, and 1-token pages, are repacked into
+                                16-token pages in the workspace first */
   int64_t num_pages;         /* page_count of each pool */
   int32_t max_pages_per_seq; /* row stride of block_tables */
   int32_t max_q_len;         /* >= every q_len (host-side bound, sizes the grid) */

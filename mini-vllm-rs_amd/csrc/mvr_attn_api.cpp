@@ -201,12 +201,17 @@ mvr::PagedAttentionPlan make_plan(const mvr_paged_attention_args* a, bool allow_
   // MVR_ATTN_PREFILL_KERNEL=false keeps every call on the split-context kernel.
   static const bool prefill_enabled = env_bool("MVR_ATTN_PREFILL_KERNEL", true);
   // (Its loads take 16-token runs, 8 in F32, inside one page: page sizes
-  // that are multiples of 16, as every size is after the repack.)
+  // that are multiples of 16, as every size is after the repack; or, at
+  // head_dim 64 and 128, each load's few whole token rows inside one page:
+  // page sizes that prefill_token_pages_supported accepts.)
   const bool page_runs = a->page_size % mvr::kChunkTokens == 0;
+  const bool prefill_pages =
+      page_runs || mvr::prefill_token_pages_supported(a->page_size, a->head_dim, a->dtype == MVR_DTYPE_F16 ? 2 : 4);
   // Other page sizes reach make_plan only for calls that the split-context
-  // kernel serves, which then reads them in place (token pages).
+  // kernel serves, which then reads them in place (token pages), or that the
+  // prefill kernel reads in place.
   plan.token_pages = !page_runs;
-  if (allow_prefill && prefill_enabled && (rows_max > 64 || force_prefill) && page_runs &&
+  if (allow_prefill && prefill_enabled && (rows_max > 64 || force_prefill) && prefill_pages &&
       mvr::prefill_head_dim_supported(a->head_dim)) {
     plan.prefill = true;
     plan.row_tiles = (int)((rows_max + mvr::kPrefillBlockRows - 1) / mvr::kPrefillBlockRows);
@@ -758,12 +763,15 @@ struct RepackPlan {
 };
 
 // Page sizes that are not a multiple of 16 are read in place by the
-// split-context kernel (token pages) down to 2 tokens per page; a call that
-// would use the chunked-prefill kernel (whose loads need 16-token runs inside
-// a page) or pages of one token is repacked into 16-token pages first.
+// split-context kernel (token pages) down to 2 tokens per page, and by the
+// chunked-prefill kernel where each of its loads' whole token rows lie in one
+// page (prefill_token_pages_supported); a call that would use the
+// chunked-prefill kernel with other page sizes, or pages of one token, is
+// repacked into 16-token pages first.
 bool needs_repack(const mvr_paged_attention_args* a) {
   if (a->page_size % mvr::kChunkTokens == 0) return false;
   if (a->page_size < 2 || !mvr::head_dim_all_plans(a->head_dim)) return true;
+  if (mvr::prefill_token_pages_supported(a->page_size, a->head_dim, a->dtype == MVR_DTYPE_F16 ? 2 : 4)) return false;
   mvr_paged_attention_args b = *a;
   b.page_size = mvr::kChunkTokens; // the plan the repacked call would take
   const CallPlan c = make_call_plan(&b);

@@ -181,7 +181,7 @@ struct Tile {
 
 // One (sequence, kv head, 128-row tile, key split): each step stages one
 // key tile per group, then QK^T, softmax and PV in turn.
-template <int D, typename T, int TT, int G>
+template <int D, typename T, int TT, int G, bool TP>
 __device__ __forceinline__ void prefill_tile_serial(const PrefillParams& p, const SeqRows& s, int b, int h, int rt,
                                                     int split, int kv_splits) {
   static_assert(G == 1 || G == 2, "one or two wavefront groups");
@@ -261,7 +261,8 @@ __device__ __forceinline__ void prefill_tile_serial(const PrefillParams& p, cons
 
   // Page arithmetic by a multiply and a shift (wave-uniform: scalar
   // instructions once per step); the host routes page sizes that are
-  // multiples of 16 to this kernel.
+  // multiples of 16 to this kernel, and (TP, token pages) other sizes that
+  // are a multiple of the tokens one load covers.
   auto page_div = [&](int tok) { return (int)(((uint64_t)(uint32_t)tok * p.page_magic) >> p.page_magic_shift); };
   auto page_mod = [&](int tok) { return tok - page_div(tok) * p.page_size; };
 
@@ -279,8 +280,14 @@ __device__ __forceinline__ void prefill_tile_serial(const PrefillParams& p, cons
   // scalar block-table load, one page address and one bound per wavefront
   // and step.  That page row goes into the buffer base, so a lane's byte
   // offset within the wavefront's tokens never changes and the loop spends no
-  // vector instructions on addresses.
+  // vector instructions on addresses.  With token pages (TP) each load u
+  // covers kLoadTokens whole token rows (head_dim 64 and 128), which lie in
+  // one page because the page size is a multiple of kLoadTokens: one
+  // block-table load, page address and bound per load and step, and the
+  // lane's offset counts from the load's first token.
   constexpr int kWaveTokens = TL::kChunksPerThread * 64 / TL::kChunksPerRow; // R
+  constexpr int kLoadTokens = 64 / TL::kChunksPerRow;
+  static_assert(!TP || 64 % TL::kChunksPerRow == 0, "token pages need loads of whole token rows");
   const int ld_t0 = wave * kWaveTokens;
   uint32_t off_k[TL::kChunksPerThread], off_v[TL::kChunksPerThread];
 #pragma unroll
@@ -288,8 +295,9 @@ __device__ __forceinline__ void prefill_tile_serial(const PrefillParams& p, cons
     const int P = (wave * TL::kChunksPerThread + u) * 64 + l;
     const int t = P / TL::kChunksPerRow, cs = P % TL::kChunksPerRow;
     const int dt = t - ld_t0;
-    off_k[u] = (uint32_t)(dt * D + TL::kChunkElems * (cs ^ TL::kswz(t))) * sizeof(T);
-    off_v[u] = (uint32_t)(dt * D + TL::kChunkElems * (2 * ((cs >> 1) ^ TL::vswz(t)) + (cs & 1))) * sizeof(T);
+    const int dl = TP ? dt - u * kLoadTokens : dt; // token row from the buffer's base
+    off_k[u] = (uint32_t)(dl * D + TL::kChunkElems * (cs ^ TL::kswz(t))) * sizeof(T);
+    off_v[u] = (uint32_t)(dl * D + TL::kChunkElems * (2 * ((cs >> 1) ^ TL::vswz(t)) + (cs & 1))) * sizeof(T);
   }
   // Branch-free: every stage issues the same loads.  A group's buffer ends at
   // the call's last key, so lanes of a group that straddles the end read
@@ -304,25 +312,50 @@ __device__ __forceinline__ void prefill_tile_serial(const PrefillParams& p, cons
   // anyway.
   const int n_steps = (j1 - j0 + G - 1) / G;
   const int i_last = max(n_steps - 1, 0);
+  constexpr int kPageLoads = TP ? TL::kChunksPerThread : 1; // block-table entries per wavefront and step
   struct Pages {
-    int64_t pg;
+    int64_t pg[kPageLoads];
+  };
+  // First token of load u (of the wavefront's tokens without TP), or the
+  // call's last key past the end.
+  auto load_token = [&](int si, int u) {
+    return min((j0 + G * si) * kTileTokens + ld_t0 + u * kLoadTokens, s.key_end - 1);
   };
   auto fetch_pages = [&](int si) {
-    return Pages{bt[page_div(min((j0 + G * si) * kTileTokens + ld_t0, s.key_end - 1))]}; // wave-uniform
+    Pages pages;
+#pragma unroll
+    for (int u = 0; u < kPageLoads; u++) pages.pg[u] = bt[page_div(load_token(si, u))]; // wave-uniform
+    return pages;
   };
   auto issue_stage = [&](int si, const Pages& pages, T* kb, T* vb) {
-    // All wave-uniform: the wavefront's first token (the last key past the
-    // end), its page row, and the bytes from there to the end of the page or
-    // of the call's keys.
-    const int tc = min((j0 + G * si) * kTileTokens + ld_t0, s.key_end - 1);
-    const int row0 = page_mod(tc);
-    const int64_t base = ((pages.pg * p.num_kv_heads + h) * p.page_size + row0) * D;
-    const uint32_t bytes = (uint32_t)min(p.page_size - row0, s.key_end - tc) * D * (uint32_t)sizeof(T);
+    if constexpr (TP) {
+      // Per load, all wave-uniform: its first token, that token's page row,
+      // and the bytes from there to the end of the page or of the call's
+      // keys.
 #pragma unroll
-    for (int u = 0; u < TL::kChunksPerThread; u++) {
-      const int dst = (wave * TL::kChunksPerThread + u) * 64 * TL::kChunkElems;
-      load_page_to_lds16(kpool + base, bytes, off_k[u], kb + dst);
-      load_page_to_lds16(vpool + base, bytes, off_v[u], vb + dst);
+      for (int u = 0; u < TL::kChunksPerThread; u++) {
+        const int tc = load_token(si, u);
+        const int row0 = page_mod(tc);
+        const int64_t base = ((pages.pg[u] * p.num_kv_heads + h) * p.page_size + row0) * D;
+        const uint32_t bytes = (uint32_t)min(p.page_size - row0, s.key_end - tc) * D * (uint32_t)sizeof(T);
+        const int dst = (wave * TL::kChunksPerThread + u) * 64 * TL::kChunkElems;
+        load_page_to_lds16(kpool + base, bytes, off_k[u], kb + dst);
+        load_page_to_lds16(vpool + base, bytes, off_v[u], vb + dst);
+      }
+    } else {
+      // All wave-uniform: the wavefront's first token (the last key past the
+      // end), its page row, and the bytes from there to the end of the page or
+      // of the call's keys.
+      const int tc = min((j0 + G * si) * kTileTokens + ld_t0, s.key_end - 1);
+      const int row0 = page_mod(tc);
+      const int64_t base = ((pages.pg[0] * p.num_kv_heads + h) * p.page_size + row0) * D;
+      const uint32_t bytes = (uint32_t)min(p.page_size - row0, s.key_end - tc) * D * (uint32_t)sizeof(T);
+#pragma unroll
+      for (int u = 0; u < TL::kChunksPerThread; u++) {
+        const int dst = (wave * TL::kChunksPerThread + u) * 64 * TL::kChunkElems;
+        load_page_to_lds16(kpool + base, bytes, off_k[u], kb + dst);
+        load_page_to_lds16(vpool + base, bytes, off_v[u], vb + dst);
+      }
     }
   };
   constexpr int kLoadsPerStage = 2 * TL::kChunksPerThread; // per lane
@@ -805,10 +838,10 @@ constexpr int prefill_tile_tokens() {
 // one (sequence, kv head) pair sit on the same XCD, so their shared K/V stays
 // in that XCD's L2 (with fewer pairs than XCDs, plain linear order keeps
 // every XCD busy).  Catch-up blocks follow the main grid.
-template <int D, typename T, int G>
+template <int D, typename T, int G, bool TP>
 __device__ __forceinline__ void prefill_tile(const PrefillParams& p, const SeqRows& s, int b, int h, int rt, int split,
                                              int kv_splits) {
-  prefill_tile_serial<D, T, prefill_tile_tokens<D, T>(), G>(p, s, b, h, rt, split, kv_splits);
+  prefill_tile_serial<D, T, prefill_tile_tokens<D, T>(), G, TP>(p, s, b, h, rt, split, kv_splits);
 }
 
 __host__ __device__ __forceinline__ int64_t prefill_main_blocks(const PrefillParams& p) {
@@ -817,7 +850,9 @@ __host__ __device__ __forceinline__ int64_t prefill_main_blocks(const PrefillPar
   return pairs >= kXcds ? kXcds * ((pairs + kXcds - 1) / kXcds) * per_pair : pairs * per_pair;
 }
 
-template <int D, typename T, int G>
+// TP: pages that are not a multiple of 16 tokens, read in place (head_dim 64
+// and 128; the page size a multiple of the tokens one load covers).
+template <int D, typename T, int G, bool TP>
 __global__ __launch_bounds__(kRowWaves* G * 64, (G == 1 && D <= 128) ? 2 : 1) void paged_prefill_kernel(PrefillParams p) {
   const int x = blockIdx.x;
   const int main_seqs = p.seq_count ? p.seq_count : p.num_seqs;
@@ -830,7 +865,7 @@ __global__ __launch_bounds__(kRowWaves* G * 64, (G == 1 && D <= 128) ? 2 : 1) vo
     if (s.q_len <= 0) return;
     for (int h = 0; h < p.num_kv_heads; h++)
       for (int rt = 0; rt < p.row_tiles; rt++) {
-        prefill_tile<D, T, G>(p, s, b, h, rt, 0, 1);
+        prefill_tile<D, T, G, TP>(p, s, b, h, rt, 0, 1);
         __syncthreads(); // group 0's hand-off reads end before the next tile refills the stages
       }
     return;
@@ -872,7 +907,7 @@ __global__ __launch_bounds__(kRowWaves* G * 64, (G == 1 && D <= 128) ? 2 : 1) vo
       rt = p.row_tiles - 1 - idx;
     }
   }
-  prefill_tile<D, T, G>(p, s, b, h, rt, split, p.kv_splits);
+  prefill_tile<D, T, G, TP>(p, s, b, h, rt, split, p.kv_splits);
 }
 
 // Merges the kv_splits partial results of every block tile:
@@ -978,13 +1013,25 @@ template <int D, typename T>
 hipError_t launch_typed(const PrefillParams& params, hipStream_t stream) {
   constexpr int TT = prefill_tile_tokens<D, T>();
   const int64_t blocks = prefill_main_blocks(params) + params.catch_count;
-  if constexpr (D > 128) {
+  if (params.page_size % 16 != 0) {
+    if (!prefill_token_pages_supported(params.page_size, D, (int)sizeof(T))) return hipErrorInvalidValue;
+    if constexpr (D == 64 || D == 128) {
+      if (params.groups == 1)
+        hipLaunchKernelGGL((paged_prefill_kernel<D, T, 1, true>), dim3((unsigned)blocks), dim3(kRowWaves * 64),
+                           0, stream, params);
+      else if (params.groups == 2)
+        hipLaunchKernelGGL((paged_prefill_kernel<D, T, 2, true>), dim3((unsigned)blocks),
+                           dim3(kRowWaves * 2 * 64), 0, stream, params);
+      else
+        return hipErrorInvalidValue;
+    }
+  } else if constexpr (D > 128) {
     if (params.groups != 1) return hipErrorInvalidValue;
-    hipLaunchKernelGGL((paged_prefill_kernel<D, T, 1>), dim3((unsigned)blocks), dim3(kRowWaves * 64), 0, stream, params);
+    hipLaunchKernelGGL((paged_prefill_kernel<D, T, 1, false>), dim3((unsigned)blocks), dim3(kRowWaves * 64), 0, stream, params);
   } else if (params.groups == 1) {
-    hipLaunchKernelGGL((paged_prefill_kernel<D, T, 1>), dim3((unsigned)blocks), dim3(kRowWaves * 64), 0, stream, params);
+    hipLaunchKernelGGL((paged_prefill_kernel<D, T, 1, false>), dim3((unsigned)blocks), dim3(kRowWaves * 64), 0, stream, params);
   } else if (params.groups == 2) {
-    hipLaunchKernelGGL((paged_prefill_kernel<D, T, 2>), dim3((unsigned)blocks), dim3(kRowWaves * 2 * 64), 0, stream,
+    hipLaunchKernelGGL((paged_prefill_kernel<D, T, 2, false>), dim3((unsigned)blocks), dim3(kRowWaves * 2 * 64), 0, stream,
                        params);
   } else {
     return hipErrorInvalidValue;

@@ -23,7 +23,9 @@ struct PrefillParams {
   int64_t out_stride_head, out_stride_token;
   float* partial_o;  // [slots][128][head_dim] fp32 when kv_splits > 1
   float* partial_ml; // [slots][128][2]
-  int32_t num_seqs, num_kv_heads, group_size, page_size; // page_size: a multiple of 16
+  // page_size: a multiple of 16, or one that prefill_token_pages_supported
+  // accepts (read in place by the token-page kernels).
+  int32_t num_seqs, num_kv_heads, group_size, page_size;
   // Page of a token without a divide: page = tok * page_magic >> page_magic_shift
   // for every tok in [0, 2^31) (page_divider).
   uint64_t page_magic;
@@ -70,6 +72,18 @@ inline void page_divider(int32_t d, uint64_t& magic, int32_t& shift) {
 // (F16 in 64-token key tiles, F32 in 32-token tiles; rows of more than 128
 // elements in blocks of one wavefront group, one wavefront per SIMD).
 constexpr bool prefill_head_dim_supported(int d) { return d >= 32 && d <= 256 && d % 32 == 0; }
+
+// Tokens that one 64-lane direct-to-LDS load of the prefill kernel covers
+// (16 bytes per lane, whole token rows at head_dim 64 and 128).
+constexpr int prefill_tokens_per_load(int d, int elem_bytes) { return 64 * 16 / (d * elem_bytes); }
+
+// Page sizes that are not a multiple of 16 which the prefill kernel reads in
+// place (token pages): head_dim 64 and 128, page sizes that are a multiple
+// of the tokens per load (so that every load's tokens lie in one page:
+// F16 D=128 multiples of 4, F16 D=64 of 8, F32 D=128 of 2, F32 D=64 of 4).
+constexpr bool prefill_token_pages_supported(int page_size, int d, int elem_bytes) {
+  return (d == 64 || d == 128) && page_size >= 2 && page_size % prefill_tokens_per_load(d, elem_bytes) == 0;
+}
 
 // f32: F32 Q/K/V/out (v_mfma_f32_32x32x2_f32); otherwise F16.
 hipError_t launch_paged_prefill(const PrefillParams& params, int head_dim, bool f32, hipStream_t stream);

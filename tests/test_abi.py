@@ -160,8 +160,10 @@ def test_workspace_too_small_is_rejected():
 def test_page_sizes_off_16_in_place_or_repacked():
     # Any page size is accepted (the reference's own tests use 2 and 3).  Decode-sized calls read pages of 2 or
     # more tokens in place: the workspace holds only their partials, as with 16-token pages.  Calls that take
-    # the chunked-prefill kernel, and pages of one token, repack each sequence's tokens into 16-token pages in
-    # the workspace first, then run the plan of that layout.
+    # the chunked-prefill kernel read them in place where each of its 64-lane loads' token rows lie in one page
+    # (head_dim 64 and 128, page sizes a multiple of the tokens per load); those calls with other page sizes,
+    # and pages of one token, repack each sequence's tokens into 16-token pages in the workspace first, then run
+    # the plan of that layout.
     pool = 2 * 64 * 8 * 16 * 128 * 2  # sequences x pages16 x kv heads x 16 tokens x head_dim x f16
     p16 = M.workspace_size(_args(max_seq_len=1024))
     assert M.workspace_size(_args(max_seq_len=1024, page_size=3, max_pages_per_seq=342)) == p16
@@ -176,6 +178,21 @@ def test_page_sizes_off_16_in_place_or_repacked():
     prefill16 = M.workspace_size(_args(max_seq_len=1024, max_q_len=256))
     assert M.workspace_size(_args(max_seq_len=1024, max_q_len=256, page_size=3, max_pages_per_seq=342)) >= \
         2 * pool + 2 * 64 * 4 + prefill16
+    # In place: F16 D=128 loads cover 4 tokens (multiples of 4), D=64 8, F32 D=128 2, F32 D=64 4.
+    in_place = [(M.DTYPE_F16, 128, 4), (M.DTYPE_F16, 128, 8), (M.DTYPE_F16, 128, 12), (M.DTYPE_F16, 64, 8),
+                (M.DTYPE_F16, 64, 24), (M.DTYPE_F32, 128, 2), (M.DTYPE_F32, 128, 6), (M.DTYPE_F32, 64, 4)]
+    repacked = [(M.DTYPE_F16, 128, 6), (M.DTYPE_F16, 64, 4), (M.DTYPE_F16, 64, 12), (M.DTYPE_F32, 128, 3),
+                (M.DTYPE_F32, 64, 2), (M.DTYPE_F16, 96, 8)]
+    for dtype, d, ps in in_place + repacked:
+        kw = dict(dtype=dtype, head_dim=d, q_stride_head=2 * d, q_stride_token=d, out_stride_head=2 * d,
+                  out_stride_token=d, max_seq_len=1024, max_q_len=256)
+        base = M.workspace_size(_args(**kw))
+        got = M.workspace_size(_args(page_size=ps, max_pages_per_seq=-(-1024 // ps), **kw))
+        es = 2 if dtype == M.DTYPE_F16 else 4
+        if (dtype, d, ps) in in_place:
+            assert got == base, (dtype, d, ps, got, base)
+        else:
+            assert got >= 2 * (2 * 64 * 8 * 16 * d * es) + base, (dtype, d, ps, got, base)
     # A page size that does not cover max_seq_len is still the reference's error.
     rc, err = _call(_args(max_seq_len=1024, page_size=3, max_pages_per_seq=300))
     assert rc == M.MVR_E_PAGES_UNCOVERED and "leaving 124 tokens uncovered" in err

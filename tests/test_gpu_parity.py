@@ -515,6 +515,48 @@ def test_uniform_batch_in_small_pages_matches_oracle(page_size, dtype, hq, hkv, 
     assert np.isfinite(got).all() and err <= (2e-3 if dtype == "f16" else 1e-5)
 
 
+@pytest.mark.parametrize("hints", [False, True])
+@pytest.mark.parametrize("dtype,hq,hkv,d,page_size", [
+    ("f16", 28, 4, 128, 4), ("f16", 28, 4, 128, 8), ("f16", 28, 4, 128, 12), ("f16", 28, 4, 128, 24),
+    ("f16", 14, 2, 64, 8), ("f16", 14, 2, 64, 40), ("f32", 28, 4, 128, 2), ("f32", 28, 4, 128, 6),
+    ("f32", 14, 2, 64, 4), ("f32", 14, 2, 64, 12)])
+def test_prefill_token_pages_match_oracle_and_16_token_pages(dtype, hq, hkv, d, page_size, hints):
+    # Page sizes that are not a multiple of 16 but a multiple of the tokens one 64-lane load of the prefill
+    # kernel covers (F16 D=128: 4, D=64: 8; F32 D=128: 2, D=64: 4) run the prefill kernel in place, each load
+    # with its own page: chunks with and without a cached prefix, a long context whose keys are split across
+    # blocks and merged, and a decode row.  With host hints the decode row runs in a launch of its own (the
+    # split-context kernel's token pages, whose partitions may differ from the 16-token plan's) beside the
+    # prefill launch.  Every row within the bar of the oracle; the prefill kernel's rows (all of them without
+    # hints) bit for bit the 16-token-page result.
+    q_lens = [200, 64, 130, 1, 96]
+    seq_lens = [700, 64, 130 + 5 * page_size + 3, 333, 96 + 6000 + page_size // 2]
+    q, layouts = _same_tokens_two_page_sizes(800 + page_size + d, dtype, hq, hkv, d, seq_lens, q_lens, page_size)
+    cu = np.concatenate([[0], np.cumsum(q_lens)]).astype(np.int32)
+    kw = dict(seq_lens_host=np.asarray(seq_lens, np.int32), cu_q_lens_host=cu) if hints else {}
+    say(f"[prefill token pages {page_size}] {dtype} D={d} hints={hints}: q {q_lens} seq {seq_lens}")
+    outs = []
+    for P, kp, vp, bt in layouts:
+        out = M.paged_attention(torch.from_numpy(q).cuda(), torch.from_numpy(kp).cuda(), torch.from_numpy(vp).cuda(),
+                                torch.from_numpy(bt).cuda(), torch.tensor(seq_lens, dtype=torch.int32).cuda(),
+                                torch.from_numpy(cu).cuda(), max_q_len=max(q_lens), max_seq_len=max(seq_lens),
+                                sum_seq_lens=int(sum(seq_lens)), **kw)
+        torch.cuda.synchronize()
+        outs.append(out.cpu().numpy())
+    P, kp, vp, bt = layouts[0]
+    ref = O.paged_attention(q, kp, vp, bt, np.asarray(seq_lens, np.int32), cu, hq, hkv, d, P,
+                            dtype=O.F16 if dtype == "f16" else O.F32, num_threads=16)
+    finite = bool(np.isfinite(outs[0]).all())
+    err = float(np.abs(outs[0].astype(np.float64) - ref).max()) if finite else float("inf")
+    view = np.uint16 if dtype == "f16" else np.uint32
+    rows = np.ones(int(cu[-1]), bool)
+    if hints:
+        rows[cu[3]:cu[4]] = False  # the decode row's launch
+    diff = int(np.count_nonzero(outs[0][:, rows].view(view) != outs[1][:, rows].view(view)))
+    say(f"[prefill token pages {page_size}] {dtype} D={d} hints={hints}: max-abs vs oracle {err:.3e}; "
+        f"{diff} prefill-kernel outputs differ from 16-token pages")
+    assert finite and err <= (2e-3 if dtype == "f16" else 1e-5) and diff == 0
+
+
 @pytest.mark.parametrize("page_size", [48, 80, 272])
 @pytest.mark.parametrize("dtype,hq,hkv,d", [("f16", 28, 4, 128), ("f32", 14, 2, 64)])
 def test_prefill_page_sizes_multiple_of_16_match_oracle_and_16_token_pages(page_size, dtype, hq, hkv, d):

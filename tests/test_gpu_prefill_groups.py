@@ -5,8 +5,9 @@ key tiles and merge at the end (two wavefronts per SIMD behind one barrier), or 
 steps through every key tile (two such blocks per CU).  The planner takes one group for F16 grids of at least 4
 blocks per CU and two otherwise; MVR_ATTN_PREFILL_GROUPS forces either (read once per process, so each shape runs
 in a child process).  Both must meet the same bar against the oracle: 2e-3 (F16) / 1e-5 (F32).  Cases: the
-Qwen2-7B chunk in F16 and F32, ragged chunks on long contexts at D=64 (key splits and their merge), and a mixed
-decode + prefill batch with host hints (the prefill launch of two); and, in this process, a batch whose grid
+Qwen2-7B chunk in F16 and F32, ragged chunks on long contexts at D=64 (key splits and their merge), a mixed
+decode + prefill batch with host hints (the prefill launch of two), and the chunk and the mixed batch in pages of
+8 (F16) and 2 (F32) tokens, which the prefill kernel reads in place; and, in this process, a batch whose grid
 (48 sequences x 16 KV heads x 2 row tiles) takes one group by the planner's own rule.
 """
 import os
@@ -56,6 +57,11 @@ CASES = {
     "qwen2-7b-chunk-f32": (lambda: W.qwen2_7b_chunked_prefill_f16("f32"), False),
     "ragged-chunks-d64": (_ragged_chunks_d64, False),
     "mixed-with-hints": (lambda: W.llama3_8b_mixed_decode_prefill_f16(num_decode=15, decode_ctx=2048), True),
+    # pages of 8 and 2 tokens, read in place (token pages)
+    "qwen2-7b-chunk-f16-p8": (lambda: W.repaged(W.qwen2_7b_chunked_prefill_f16(), 8), False),
+    "qwen2-7b-chunk-f32-p2": (lambda: W.repaged(W.qwen2_7b_chunked_prefill_f16("f32"), 2), False),
+    "mixed-with-hints-p8": (lambda: W.repaged(W.llama3_8b_mixed_decode_prefill_f16(num_decode=15, decode_ctx=2048), 8),
+                            True),
 }
 
 
