@@ -206,7 +206,8 @@ mvr::PagedAttentionPlan make_plan(const mvr_paged_attention_args* a, bool allow_
   // page sizes that prefill_token_pages_supported accepts.)
   const bool page_runs = a->page_size % mvr::kChunkTokens == 0;
   const bool prefill_pages =
-      page_runs || mvr::prefill_token_pages_supported(a->page_size, a->head_dim, a->dtype == MVR_DTYPE_F16 ? 2 : 4);
+      page_runs || mvr::prefill_token_pages_supported(a->page_size, a->num_kv_heads, a->head_dim,
+                                                      a->dtype == MVR_DTYPE_F16 ? 2 : 4);
   // Other page sizes reach make_plan only for calls that the split-context
   // kernel serves, which then reads them in place (token pages), or that the
   // prefill kernel reads in place.
@@ -771,7 +772,8 @@ struct RepackPlan {
 bool needs_repack(const mvr_paged_attention_args* a) {
   if (a->page_size % mvr::kChunkTokens == 0) return false;
   if (a->page_size < 2 || !mvr::head_dim_all_plans(a->head_dim)) return true;
-  if (mvr::prefill_token_pages_supported(a->page_size, a->head_dim, a->dtype == MVR_DTYPE_F16 ? 2 : 4)) return false;
+  if (mvr::prefill_token_pages_supported(a->page_size, a->num_kv_heads, a->head_dim, a->dtype == MVR_DTYPE_F16 ? 2 : 4))
+    return false;
   mvr_paged_attention_args b = *a;
   b.page_size = mvr::kChunkTokens; // the plan the repacked call would take
   const CallPlan c = make_call_plan(&b);

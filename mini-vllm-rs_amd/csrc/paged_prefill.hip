@@ -331,16 +331,21 @@ __device__ __forceinline__ void prefill_tile_serial(const PrefillParams& p, cons
     if constexpr (TP) {
       // Per load, all wave-uniform: its first token, that token's page row,
       // and the bytes from there to the end of the page or of the call's
-      // keys.
+      // keys.  Byte offsets: one 32 x 32 -> 64-bit product for the page (a
+      // page of all KV heads is below 4 GiB, checked on the host), 32 bits
+      // within it.
+      constexpr uint32_t kRowBytes = D * (uint32_t)sizeof(T);
+      const uint32_t page_bytes = (uint32_t)(p.num_kv_heads * p.page_size) * kRowBytes;
+      const uint32_t head_bytes = (uint32_t)(h * p.page_size) * kRowBytes;
 #pragma unroll
       for (int u = 0; u < TL::kChunksPerThread; u++) {
         const int tc = load_token(si, u);
         const int row0 = page_mod(tc);
-        const int64_t base = ((pages.pg[u] * p.num_kv_heads + h) * p.page_size + row0) * D;
-        const uint32_t bytes = (uint32_t)min(p.page_size - row0, s.key_end - tc) * D * (uint32_t)sizeof(T);
+        const uint64_t base = (uint64_t)(uint32_t)pages.pg[u] * page_bytes + (head_bytes + (uint32_t)row0 * kRowBytes);
+        const uint32_t bytes = (uint32_t)min(p.page_size - row0, s.key_end - tc) * kRowBytes;
         const int dst = (wave * TL::kChunksPerThread + u) * 64 * TL::kChunkElems;
-        load_page_to_lds16(kpool + base, bytes, off_k[u], kb + dst);
-        load_page_to_lds16(vpool + base, bytes, off_v[u], vb + dst);
+        load_page_to_lds16(reinterpret_cast<const char*>(kpool) + base, bytes, off_k[u], kb + dst);
+        load_page_to_lds16(reinterpret_cast<const char*>(vpool) + base, bytes, off_v[u], vb + dst);
       }
     } else {
       // All wave-uniform: the wavefront's first token (the last key past the
@@ -1014,7 +1019,8 @@ hipError_t launch_typed(const PrefillParams& params, hipStream_t stream) {
   constexpr int TT = prefill_tile_tokens<D, T>();
   const int64_t blocks = prefill_main_blocks(params) + params.catch_count;
   if (params.page_size % 16 != 0) {
-    if (!prefill_token_pages_supported(params.page_size, D, (int)sizeof(T))) return hipErrorInvalidValue;
+    if (!prefill_token_pages_supported(params.page_size, params.num_kv_heads, D, (int)sizeof(T)))
+      return hipErrorInvalidValue;
     if constexpr (D == 64 || D == 128) {
       if (params.groups == 1)
         hipLaunchKernelGGL((paged_prefill_kernel<D, T, 1, true>), dim3((unsigned)blocks), dim3(kRowWaves * 64),

@@ -80,9 +80,12 @@ constexpr int prefill_tokens_per_load(int d, int elem_bytes) { return 64 * 16 / 
 // Page sizes that are not a multiple of 16 which the prefill kernel reads in
 // place (token pages): head_dim 64 and 128, page sizes that are a multiple
 // of the tokens per load (so that every load's tokens lie in one page:
-// F16 D=128 multiples of 4, F16 D=64 of 8, F32 D=128 of 2, F32 D=64 of 4).
-constexpr bool prefill_token_pages_supported(int page_size, int d, int elem_bytes) {
-  return (d == 64 || d == 128) && page_size >= 2 && page_size % prefill_tokens_per_load(d, elem_bytes) == 0;
+// F16 D=128 multiples of 4, F16 D=64 of 8, F32 D=128 of 2, F32 D=64 of 4),
+// and pages (all KV heads) of less than 4 GiB, whose byte offsets the
+// kernel keeps in 32 bits.
+constexpr bool prefill_token_pages_supported(int page_size, int num_kv_heads, int d, int elem_bytes) {
+  return (d == 64 || d == 128) && page_size >= 2 && page_size % prefill_tokens_per_load(d, elem_bytes) == 0 &&
+         (long long)num_kv_heads * page_size * d * elem_bytes < (1LL << 32);
 }
 
 // f32: F32 Q/K/V/out (v_mfma_f32_32x32x2_f32); otherwise F16.
