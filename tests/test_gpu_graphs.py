@@ -1,5 +1,6 @@
 """The attention entry points captured in a HIP graph: every plan's launches (split-context kernel and merge, block
-merge, 32-row verify tiles, chunked prefill with key splits and their merge in F16 and F32, the page repack)
+merge, 32-row verify tiles, chunked prefill with key splits and their merge in F16 and F32, the prefill kernel
+on 8- and 2-token pages read in place, the page repack)
 replay from the graph bit for bit like the eager call.  Serving loops capture their decode step this way to cut
 launch overhead; the library makes no allocation, memset or synchronisation on these paths, so capture records
 kernels only.
@@ -55,6 +56,10 @@ CASES = {
                                             page_size=5),
     "repacked-page-size-5": lambda: _ragged("page size 5 prefill", "f16", 32, 8, 128, [700, 300], [1, 100],
                                             page_size=5),
+    "prefill-token-pages-8": lambda: _ragged("page size 8 prefill", "f16", 32, 8, 128, [700, 300], [1, 100],
+                                             page_size=8),
+    "prefill-token-pages-2-key-splits-f32": lambda: _ragged("page size 2 prefill f32", "f32", 32, 8, 128, [4000],
+                                                            [130], page_size=2),
     "head-dim-96-f32": lambda: _ragged("head_dim 96", "f32", 32, 8, 96, [700, 97, 1500], [1, 5, 40]),
 }
 

@@ -72,7 +72,7 @@ def _long_prefill(dtype):
 
 @pytest.mark.parametrize("case", ["page-size-5-in-place", "repacked-page-size-5", "head-dim-96-repacked",
                                   "mixed-with-hints", "block-merge", "prefill", "prefill-f32", "prefill-key-splits-f16",
-                                  "prefill-key-splits-f32"])
+                                  "prefill-key-splits-f32", "prefill-token-pages-8"])
 def test_noalloc_equals_workspace_call_on_every_plan(case):
     if case in ("page-size-5-in-place", "repacked-page-size-5", "head-dim-96-repacked"):
         # decode and verify rows read 5-token pages in place; with a 100-token chunk the call is prefill-sized
@@ -99,6 +99,10 @@ def test_noalloc_equals_workspace_call_on_every_plan(case):
     elif case.startswith("prefill-key-splits"):
         w = _long_prefill(case.rsplit("-", 1)[1])
         t = W.device_tensors(w, None, seed=9)
+    elif case == "prefill-token-pages-8":
+        # the prefill kernel reads 8-token pages in place: no repack in the scratch
+        w = W.repaged(W.qwen2_7b_chunked_prefill_f16(), 8)
+        t = W.device_tensors(w, None, seed=10)
     else:
         w = W.qwen2_7b_chunked_prefill_f16("f32" if case == "prefill-f32" else "f16")
         t = W.device_tensors(w, None, seed=7)
