@@ -767,11 +767,14 @@ struct RepackPlan {
 // split-context kernel (token pages) down to 2 tokens per page, and by the
 // chunked-prefill kernel where each of its loads' whole token rows lie in one
 // page (prefill_token_pages_supported); a call that would use the
-// chunked-prefill kernel with other page sizes, or pages of one token, is
-// repacked into 16-token pages first.
+// chunked-prefill kernel with other page sizes, pages of one token, and pages
+// of 2^31 elements or more over all KV heads (token pages keep offsets within
+// a page in 32 bits) are repacked into 16-token pages first.
 bool needs_repack(const mvr_paged_attention_args* a) {
   if (a->page_size % mvr::kChunkTokens == 0) return false;
-  if (a->page_size < 2 || !mvr::head_dim_all_plans(a->head_dim)) return true;
+  if (a->page_size < 2 || !mvr::head_dim_all_plans(a->head_dim) ||
+      !mvr::token_page_offsets_fit(a->num_kv_heads, a->page_size, a->head_dim))
+    return true;
   if (mvr::prefill_token_pages_supported(a->page_size, a->num_kv_heads, a->head_dim, a->dtype == MVR_DTYPE_F16 ? 2 : 4))
     return false;
   mvr_paged_attention_args b = *a;

@@ -586,32 +586,36 @@ __global__ __launch_bounds__(kWaveSize* WPB, (kernel_min_blocks<Tr, NB, DEPTH, W
       auto pdiv = [&](int t) { return (int)(((uint64_t)(uint32_t)t * p.page_magic) >> p.page_magic_shift); };
       const int pf = pdiv(tok0);
       const int pl = pdiv(min(tok0 + kChunkTokens - 1, tmax));
-      // Row r's element offset in the pools: (page * Hkv + h) * P + slot, times D.
-      int64_t roff[1 + Tr::kLoads];
+      // Row r's element offset in the pools: (page * Hkv + h) * P + slot,
+      // times D, as page * (Hkv P D), one 32 x 32 -> 64-bit product, plus
+      // (h P + slot) D in 32 bits (a page of all KV heads holds fewer than
+      // 2^31 elements, checked on the host).
+      const uint32_t page_elems = (uint32_t)(p.num_kv_heads * p.page_size) * D;
+      const uint32_t head_elems = (uint32_t)(h * p.page_size);
+      uint32_t roff[1 + Tr::kLoads];
+      int pj[1 + Tr::kLoads]; // the row's page, counted from the chunk's first
 #pragma unroll
       for (int i = 0; i <= Tr::kLoads; i++) {
         const int r = i == 0 ? (l & 15) : Tr::v_row(l, i - 1);
         const int t = min(tok0 + r, tmax);
         const int pi = pdiv(t);
-        roff[i] = t - pi * p.page_size; // slot
+        roff[i] = (head_elems + (uint32_t)(t - pi * p.page_size)) * D; // (h P + slot) D
+        pj[i] = pi - pf;
       }
-      int64_t pg[1 + Tr::kLoads];
+      uint32_t pg[1 + Tr::kLoads];
 #pragma unroll
       for (int i = 0; i <= Tr::kLoads; i++) pg[i] = 0;
 #pragma unroll
       for (int j = 0; j < kTpWindow; j++) {
         if (j > 0 && pf + j > pl) break; // the chunk's pages end here (wave-uniform)
-        const int page = __builtin_amdgcn_readfirstlane(bt[min(pf + j, pl)]);
+        const uint32_t page = (uint32_t)__builtin_amdgcn_readfirstlane(bt[min(pf + j, pl)]);
 #pragma unroll
-        for (int i = 0; i <= Tr::kLoads; i++) {
-          const int r = i == 0 ? (l & 15) : Tr::v_row(l, i - 1);
-          pg[i] = pdiv(min(tok0 + r, tmax)) - pf == j ? page : pg[i];
-        }
+        for (int i = 0; i <= Tr::kLoads; i++) pg[i] = pj[i] == j ? page : pg[i];
       }
-      Tr::load_k_row(kpool + ((pg[0] * p.num_kv_heads + h) * p.page_size + roff[0]) * D, l, kr);
+      Tr::load_k_row(kpool + ((uint64_t)pg[0] * page_elems + roff[0]), l, kr);
 #pragma unroll
       for (int u = 0; u < Tr::kLoads; u++)
-        vr[u] = Tr::load_v_row(vpool + ((pg[1 + u] * p.num_kv_heads + h) * p.page_size + roff[1 + u]) * D, l, u);
+        vr[u] = Tr::load_v_row(vpool + ((uint64_t)pg[1 + u] * page_elems + roff[1 + u]), l, u);
     } else {
       const int64_t off = slab_offset(k);
       Tr::load_k(kpool + off, l, kr);
@@ -975,6 +979,8 @@ hipError_t launch_units(const PagedAttentionPlan& plan, const PagedAttentionPara
 
 template <typename Tr, int D, int NB>
 hipError_t launch_typed(const PagedAttentionPlan& plan, const PagedAttentionParams& params, hipStream_t stream) {
+  if (plan.token_pages && !token_page_offsets_fit(params.num_kv_heads, params.page_size, D))
+    return hipErrorInvalidValue;
   if constexpr (NB == 1 && head_dim_all_plans(D)) {
     if (plan.block_merge) {
       // One block of block_waves wavefronts per (sequence, KV head, row tile).

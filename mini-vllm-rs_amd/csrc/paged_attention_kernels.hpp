@@ -21,6 +21,13 @@ constexpr int kWavesPerBlock = 4;
 constexpr bool head_dim_supported(int d) { return d >= 32 && d <= 256 && d % 32 == 0; }
 constexpr bool head_dim_all_plans(int d) { return d == 64 || d == 128; }
 
+// Token pages (page sizes that are not a multiple of 16, read in place) keep
+// the element offsets within a page of all KV heads in 32 bits: such a page
+// must hold fewer than 2^31 elements (larger ones are repacked).
+constexpr bool token_page_offsets_fit(int num_kv_heads, int page_size, int head_dim) {
+  return (long long)num_kv_heads * page_size * head_dim < (1LL << 31);
+}
+
 // One launch of the split-context kernel.  A "unit" is the work of one
 // wavefront: (sequence b, kv head h, row tile rt, context partition part).
 // Rows of a kv head are the grouped query rows rho = r*q_len + i (r = query
