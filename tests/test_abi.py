@@ -193,6 +193,11 @@ def test_page_sizes_off_16_in_place_or_repacked():
             assert got == base, (dtype, d, ps, got, base)
         else:
             assert got >= 2 * (2 * 64 * 8 * 16 * d * es) + base, (dtype, d, ps, got, base)
+    # Token pages keep offsets within a page of all KV heads in 32 bits: a decode call on pages of 2^31
+    # elements or more (8 KV heads x 2,097,153 tokens x 128) is repacked instead.
+    huge = (1 << 21) + 1
+    assert M.workspace_size(_args(max_seq_len=1024, page_size=huge - 2, max_pages_per_seq=1)) == p16
+    assert M.workspace_size(_args(max_seq_len=1024, page_size=huge, max_pages_per_seq=1)) >= 2 * pool + p16
     # A page size that does not cover max_seq_len is still the reference's error.
     rc, err = _call(_args(max_seq_len=1024, page_size=3, max_pages_per_seq=300))
     assert rc == M.MVR_E_PAGES_UNCOVERED and "leaving 124 tokens uncovered" in err
