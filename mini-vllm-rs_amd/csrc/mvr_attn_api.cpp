@@ -362,12 +362,14 @@ mvr::PagedAttentionPlan make_plan(const mvr_paged_attention_args* a, bool allow_
   // 130) and 8 Qwen2-0.5B sequences from 14.2 to 15.0 us.  It is taken when
   // the batch has many sequences and most of the slot == partition grid
   // would hold no work (estimated from the length hint), which selects the
-  // two winning cases and none of the others.  MVR_ATTN_DENSE_RAGGED=false
-  // turns it off.
+  // two winning cases and none of the others.  Token pages take it from 8
+  // tokens per page (64 ragged sequences of 2,048..14,336 tokens in 8-token
+  // pages 468 -> 431 us, the others within 1%); in 5-token pages it lost up
+  // to 3.5% on shorter contexts.  MVR_ATTN_DENSE_RAGGED=false turns it off.
   static const bool dense_enabled = env_bool("MVR_ATTN_DENSE_RAGGED", true);
   bool dense = false;
   if (dense_enabled && ragged && plan.row_tiles == 1 && plan.max_parts > 1 && !plan.block_merge && n_live >= 32 &&
-      !plan.token_pages && all_plans) {
+      (!plan.token_pages || a->page_size >= 8) && all_plans) {
     const int64_t chunk_tokens = (int64_t)mvr::kChunkTokens * plan.chunks_per_part;
     const int64_t est_live = (a->sum_seq_lens + chunk_tokens - 1) / chunk_tokens + n_live / 2;
     dense = est_live * 10 < (int64_t)a->num_seqs * plan.max_parts * 7; // live fraction < 0.7

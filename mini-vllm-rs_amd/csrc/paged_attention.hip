@@ -955,10 +955,17 @@ hipError_t launch_units(const PagedAttentionPlan& plan, const PagedAttentionPara
                        dim3(kWaveSize * WPB), 0, stream, params);
     return hipGetLastError();
   } else if (plan.token_pages) {
-    // planned with one wavefront per block, two chunks in flight, slot == partition
-    if (WPB != 1 || plan.dense_parts || plan.deep_pipeline) return hipErrorInvalidValue;
-    hipLaunchKernelGGL((paged_attention_kernel<Tr, D, NB, false, false, 2, 1, true>), dim3((unsigned)blocks),
-                       dim3(kWaveSize), 0, stream, params);
+    // planned with one wavefront per block and two chunks in flight, slot ==
+    // partition or the dense layout
+    if (WPB != 1 || plan.deep_pipeline) return hipErrorInvalidValue;
+    if (plan.dense_parts) {
+      if (params.row_tiles != 1) return hipErrorInvalidValue; // dense_unit walks row tile 0 only
+      hipLaunchKernelGGL((paged_attention_kernel<Tr, D, NB, false, true, 2, 1, true>), dim3((unsigned)blocks),
+                         dim3(kWaveSize), 0, stream, params);
+    } else {
+      hipLaunchKernelGGL((paged_attention_kernel<Tr, D, NB, false, false, 2, 1, true>), dim3((unsigned)blocks),
+                         dim3(kWaveSize), 0, stream, params);
+    }
   } else if (plan.dense_parts) {
     if (params.row_tiles != 1) return hipErrorInvalidValue; // dense_unit walks row tile 0 only
     hipLaunchKernelGGL((paged_attention_kernel<Tr, D, NB, false, true, 2, WPB>), dim3((unsigned)blocks),

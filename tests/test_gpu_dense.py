@@ -7,9 +7,10 @@ lengths (dense_unit).  Same bar as every call: 2e-3 (F16) / 1e-5 (F32)
 against the oracle.  Covers 64 sequences of 257..2049 tokens (F16, D=128), 150
 sequences of 17..1024 tokens (more than one 64-sequence block of the scan, the
 F16 D=64 kernel), 40 F32 sequences at D=64 and at D=128 (whose key rows
-of 512 bytes take the finer dense split), and, for contrast, two such batches
-in pages of 8 and 5 tokens read in place (token pages), which keep the
-slot == partition layout.  By default a dense plan also splits
+of 512 bytes take the finer dense split), and two such batches in pages of
+8 and 5 tokens read in place (token pages), of which the first takes the
+dense layout (from 8 tokens per page) and the second slot == partition.
+By default a dense plan also splits
 contexts into more partitions than the slot == partition plan of the same
 batch (a higher fill target), which changes the rounding.  With the same
 partitions the dense layout only changes which wavefront computes which
@@ -65,7 +66,8 @@ CASES = {
     "f16-d64-150x[17,1024]": ("f16", 14, 2, 64, 150, 17, 1024, 72),
     "f32-d64-40x[100,3000]": ("f32", 14, 2, 64, 40, 100, 3000, 73),
     "f32-d128-40x[512,4096]": ("f32", 32, 8, 128, 40, 512, 4096, 74),
-    # pages of 8 and 5 tokens, read in place (token pages); such batches keep the slot == partition layout
+    # pages of 8 and 5 tokens, read in place (token pages): the dense layout from 8 tokens per page, the
+    # slot == partition layout below
     "f16-d128-64x[257,2049]-p8": ("f16", 32, 8, 128, 64, 257, 2049, 75, 8),
     "f32-d64-40x[100,3000]-p5": ("f32", 14, 2, 64, 40, 100, 3000, 76, 5),
 }
@@ -116,7 +118,8 @@ _CHILD = (
 )
 
 
-FIXED_CHUNKS = {"f16-d128-64x[257,2049]": "8", "f16-d64-150x[17,1024]": "4", "f32-d128-40x[512,4096]": "8"}
+FIXED_CHUNKS = {"f16-d128-64x[257,2049]": "8", "f16-d64-150x[17,1024]": "4", "f32-d128-40x[512,4096]": "8",
+                "f16-d128-64x[257,2049]-p8": "8"}
 
 
 def _run_child(name, dst, **env):
