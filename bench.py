@@ -372,6 +372,23 @@ def measure_head_dims(W, M, torch, steps, warmup):
     return res
 
 
+RAGGED_PAGES = [(64, 2048), (32, 4096), (64, 8192), (128, 2048)]
+
+
+def measure_ragged_pages(W, M, torch, steps, warmup):
+    """Ragged decode batches (Llama-3-8B shape, F16, lengths U[ctx/4, 7 ctx/4]) in 16-, 8- and 5-token pages, the
+    smaller ones read in place (token pages).  Run once as is and once with MVR_ATTN_DENSE_RAGGED=false to
+    compare the dense layout with slot == partition."""
+    res = {}
+    for batch, ctx in RAGGED_PAGES:
+        for ps in (16, 8, 5):
+            log(f"[bench] ragged {batch} x U[{ctx // 4},{7 * ctx // 4}] in {ps}-token pages")
+            fn = (lambda b=batch, c=ctx, ps=ps: W.repaged(W.llama3_8b_decode_map_f16(b, c, True), ps)) if ps != 16 \
+                else (lambda b=batch, c=ctx: W.llama3_8b_decode_map_f16(b, c, True))
+            res[f"{batch}x{ctx}r/p{ps}"] = measure(W, M, torch, fn, steps, warmup)
+    return res
+
+
 def measure_append(W, M, torch, cfg, steps, warmup):
     w = W.CONFIGS[cfg]()
     t = W.device_tensors(w, None)
@@ -448,6 +465,8 @@ def main():
                     help="time only the Qwen2-7B fresh 8,192-token prompt (F16 prefill, one call)")
     ap.add_argument("--head-dims", action="store_true",
                     help="time only the headline decode shape at every supported head dimension")
+    ap.add_argument("--ragged-pages", action="store_true",
+                    help="time only ragged decode batches in 16-, 8- and 5-token pages")
     a = ap.parse_args()
     if a.gpus != 1:
         print(f"bench.py measures one GPU only; --gpus {a.gpus} is not supported: the attention path runs on one "
@@ -475,6 +494,9 @@ def main():
         return
     if a.head_dims:
         print(json.dumps({"head_dims": measure_head_dims(W, M, torch, a.steps, a.warmup)}), flush=True)
+        return
+    if a.ragged_pages:
+        print(json.dumps({"ragged_pages": measure_ragged_pages(W, M, torch, a.steps, a.warmup)}), flush=True)
         return
     if a.only_fresh:
         log("[bench] Qwen2-7B fresh 8,192-token prompt only")
