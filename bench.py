@@ -328,6 +328,12 @@ def measure_page_sizes(W, M, torch, steps, warmup):
         for ps in sizes:
             log(f"[bench] config {cfg} in {ps}-token pages")
             res[f"{cfg}/{ps}"] = measure(W, M, torch, lambda: W.repaged(W.CONFIGS[cfg](), ps), steps, warmup)
+    # The mixed step (63 decodes of 8,192 tokens + a 256-token chunk on 2,048): in 8-token pages both launches
+    # read in place, in 5-token pages the whole batch is repacked first.
+    for ps in (8, 5):
+        log(f"[bench] mixed decode + prefill step in {ps}-token pages")
+        res[f"mixed/{ps}"] = measure(W, M, torch, lambda: W.repaged(W.llama3_8b_mixed_decode_prefill_f16(), ps),
+                                     steps, warmup)
     return res
 
 
